@@ -1,0 +1,371 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 Q4_K / Q8_0 matmul backend (one GPU), in the style of fak's
+cmd/q8kernel / cmd/q8bench: seeded synthetic weights of each workload's shape, warm-up, timed
+launches with HIP events, a JSON report.
+
+The headline line (`value`) is the Q4_K decode GEMV at the Qwen2.5-7B FFN shape: one step = the
+gate/up GEMV (K=3584 -> N=18944) plus the down GEMV (K=18944 -> N=3584) at M=1, inputs resident
+in HBM. Throughput counts algorithmic bytes: GGUF-native weight bytes (144 B per 256 weights)
+plus f32 activations and outputs, once. Every launch reads a different copy of the weights,
+rotating over more than 256 MB so the 256 MB Infinity Cache cannot serve them.
+
+The other workloads are reported under "workloads": Q8_0 GEMV 576->1536, the prefill GEMM at
+M=128/512/2048 (TFLOP/s vs the 2.5 PFLOP/s dense f16 MFMA peak), the 28-layer Qwen2.5-7B decode
+matmul set (tokens/s bound by matmul time) and the 27B-class small-M verify widths.
+
+`cpu_baseline` times the oracle (the C restatement of the reference's Go CPU GEMV, row-parallel
+over the host cores) on the same C2 inputs.
+
+    python bench.py [--steps K] [--warmup W] [--quick] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from fak_amd import fakhip, synth  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16 MFMA
+ROTATE_BYTES = 300 << 20    # > 256 MB Infinity Cache
+METRIC = "Q4_K decode GEMV HBM GB/s (% peak); prefill GEMM TFLOP/s (% MFMA peak)"
+
+
+def q4k_bytes(n, k):
+    return n * (k // 256) * 144
+
+
+def q8_bytes(n, k):
+    return n * (k // 32) * 34
+
+
+class Events:
+    def __init__(self):
+        self.lib = fakhip.load()
+        self.pool = []
+
+    def new(self):
+        e = C.c_void_p()
+        fakhip.call("fhip_event_create", C.byref(e))
+        self.pool.append(e)
+        return e
+
+    def record(self, e):
+        fakhip.call("fhip_event_record", e)
+
+    def ms(self, a, b):
+        v = C.c_float()
+        fakhip.call("fhip_event_elapsed_ms", a, b, C.byref(v))
+        return v.value
+
+
+class Weight:
+    """A tiled device weight uploaded once and replicated to `copies` distinct buffers."""
+
+    def __init__(self, kind, n, k, seed, copies):
+        self.kind, self.n, self.k = kind, n, k
+        lib = fakhip.load()
+        if kind == "q4k":
+            raw = synth.q4k_weights(n, k, seed)
+            p0 = fakhip.alloc_call("fhip_q4k_upload", raw.ctypes.data, n, k)
+            self.nbytes = lib.fhip_q4k_packed_bytes(n, k)
+            self.alg_bytes = q4k_bytes(n, k)
+            self.fn = "fhip_q4k_matmul_f32"
+        else:
+            raw = synth.q8_0_weights(n, k, seed)
+            p0 = fakhip.alloc_call("fhip_q8_0_upload", raw.ctypes.data, n, k)
+            self.nbytes = lib.fhip_q8_0_packed_bytes(n, k)
+            self.alg_bytes = q8_bytes(n, k)
+            self.fn = "fhip_q8_0_matmul_f32"
+        self.raw = raw
+        self.ptrs = [p0]
+        for _ in range(copies - 1):
+            p = fakhip.alloc_call("fhip_malloc", self.nbytes)
+            fakhip.call("fhip_d2d", p, p0, self.nbytes)
+            self.ptrs.append(p)
+
+    def free(self):
+        for p in self.ptrs:
+            fakhip.load().fhip_free(p)
+        self.ptrs = []
+
+
+class Buf:
+    def __init__(self, nbytes, host=None):
+        self.ptr = fakhip.alloc_call("fhip_malloc", max(nbytes, 16))
+        self.nbytes = nbytes
+        if host is not None:
+            fakhip.call("fhip_h2d", self.ptr, np.ascontiguousarray(host).ctypes.data, nbytes)
+
+    def host(self, dtype=np.float32):
+        out = np.empty(self.nbytes // np.dtype(dtype).itemsize, dtype)
+        fakhip.call("fhip_d2h", out.ctypes.data, self.ptr, out.nbytes)
+        return out
+
+    def free(self):
+        fakhip.load().fhip_free(self.ptr)
+
+
+def copies_for(nbytes):
+    return max(2, -(-ROTATE_BYTES // max(nbytes, 1)))
+
+
+def time_calls(calls, steps, warmup, ev):
+    """calls: list of (fn_name, args). One step runs every call once. Returns (ms per step,
+    per-call average ms list)."""
+    lib = fakhip.load()
+    fns = [(getattr(lib, fn), args, fn) for fn, args in calls]
+
+    def run_step(i):
+        for f, args, name in fns:
+            rc = f(*args(i))
+            if rc:
+                fakhip.check(name, rc)
+
+    for i in range(warmup):
+        run_step(i)
+    fakhip.call("fhip_sync")
+    # Per-call timing pass: an event pair around every call.
+    marks = [[ev.new(), ev.new()] for _ in fns]
+    per = [0.0] * len(fns)
+    for i in range(steps):
+        for j, (f, args, name) in enumerate(fns):
+            ev.record(marks[j][0])
+            rc = f(*args(i))
+            if rc:
+                fakhip.check(name, rc)
+            ev.record(marks[j][1])
+            per[j] += ev.ms(marks[j][0], marks[j][1])
+    per = [p / steps for p in per]
+    # Whole-step timing pass: back-to-back launches bracketed by one event pair.
+    fakhip.call("fhip_sync")
+    a, b = ev.new(), ev.new()
+    ev.record(a)
+    for i in range(steps):
+        run_step(i)
+    ev.record(b)
+    total = ev.ms(a, b)
+    fakhip.call("fhip_sync")
+    return total / steps, per
+
+
+def bench_gemv_pair(steps, warmup, ev, seed=7):
+    """C2: the Qwen2.5-7B FFN decode GEMVs (gate/up 3584->18944, down 18944->3584), M=1."""
+    shapes = [(18944, 3584), (3584, 18944)]
+    ws, xs, ys = [], [], []
+    for idx, (n, k) in enumerate(shapes):
+        w = Weight("q4k", n, k, seed + idx, copies_for(q4k_bytes(n, k)))
+        x = synth.activations(1, k, seed + 10 + idx)
+        ws.append(w)
+        xs.append((x, Buf(x.nbytes, x)))
+        ys.append(Buf(n * 4))
+    calls = []
+    for idx, (n, k) in enumerate(shapes):
+        w, (_, xb), yb = ws[idx], xs[idx], ys[idx]
+        calls.append(("fhip_q4k_matmul_f32",
+                      (lambda i, w=w, xb=xb, yb=yb, n=n, k=k:
+                       (w.ptrs[i % len(w.ptrs)], xb.ptr, yb.ptr, n, k, 1))))
+    ms, per = time_calls(calls, steps, warmup, ev)
+    alg = [q4k_bytes(n, k) + 4 * (n + k) for n, k in shapes]
+    res = {
+        "ms_per_step": ms,
+        "per_call_us": [1e3 * p for p in per],
+        "per_call_GBs": [a / (p * 1e6) for a, p in zip(alg, per)],
+        "alg_bytes": alg,
+        "copies": [len(w.ptrs) for w in ws],
+    }
+    return res, ws, xs, ys
+
+
+def bench_q8_0(steps, warmup, ev):
+    n, k = 1536, 576
+    w = Weight("q8", n, k, 1, copies_for(q8_bytes(n, k)))
+    x = synth.activations(1, k, 2)
+    xb, yb = Buf(x.nbytes, x), Buf(n * 4)
+    calls = [("fhip_q8_0_matmul_f32", lambda i: (w.ptrs[i % len(w.ptrs)], xb.ptr, yb.ptr, n, k, 1))]
+    ms, per = time_calls(calls, steps, warmup, ev)
+    alg = q8_bytes(n, k) + 4 * (n + k)
+    w.free(), xb.free(), yb.free()
+    return {"shape": [1, k, n], "blocks": n * (k // 32), "us_per_call": 1e3 * per[0],
+            "us_back_to_back": 1e3 * ms, "GBs_back_to_back": alg / (ms * 1e6),
+            "alg_bytes": alg}
+
+
+def bench_gemm(M, steps, warmup, ev):
+    n, k = 18944, 3584
+    w = Weight("q4k", n, k, 3, 2)
+    X = synth.activations(M, k, 4)
+    xb, yb = Buf(X.nbytes, X), Buf(M * n * 4)
+    calls = [("fhip_q4k_matmul_f32", lambda i: (w.ptrs[i % len(w.ptrs)], xb.ptr, yb.ptr, n, k, M))]
+    ms, per = time_calls(calls, steps, warmup, ev)
+    flops = 2.0 * M * n * k
+    t = per[0] * 1e-3
+    w.free(), xb.free(), yb.free()
+    return {"M": M, "us_per_call": 1e3 * per[0], "TFLOPs": flops / t / 1e12,
+            "pct_mfma_peak": 100.0 * flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS}
+
+
+def bench_small_m(steps, warmup, ev):
+    out = []
+    shapes = [(25600, 5120), (5120, 25600)]
+    ws = [Weight("q4k", n, k, 20 + i, copies_for(q4k_bytes(n, k))) for i, (n, k) in enumerate(shapes)]
+    for M in (1, 4, 8, 16):
+        bufs = []
+        calls = []
+        for (n, k), w in zip(shapes, ws):
+            X = synth.activations(M, k, 30 + M)
+            xb, yb = Buf(X.nbytes, X), Buf(M * n * 4)
+            bufs += [xb, yb]
+            calls.append(("fhip_q4k_matmul_f32",
+                          lambda i, w=w, xb=xb, yb=yb, n=n, k=k, M=M:
+                          (w.ptrs[i % len(w.ptrs)], xb.ptr, yb.ptr, n, k, M)))
+        ms, per = time_calls(calls, steps, warmup, ev)
+        alg = sum(q4k_bytes(n, k) + 4 * M * (n + k) for n, k in shapes)
+        gbs = alg / (sum(per) * 1e6)
+        out.append({"M": M, "us_pair": 1e3 * sum(per), "GBs": gbs,
+                    "pct_hbm_peak": 100.0 * gbs / HBM_PEAK_GBS})
+        for b in bufs:
+            b.free()
+    for w in ws:
+        w.free()
+    return out
+
+
+def bench_decode_stack(steps, warmup, ev, layers=28):
+    """C4: one token of a 28-layer Qwen2.5-7B-shaped decode (q, k, v, o, gate, up, down per layer
+    + lm_head), all Q4_K, every layer at its own device address."""
+    H, KV, F, V = 3584, 512, 18944, 152064
+    layer_shapes = [(H, H), (KV, H), (KV, H), (H, H), (F, H), (F, H), (H, F)]
+    base = [Weight("q4k", n, k, 40 + i, 1) for i, (n, k) in enumerate(layer_shapes)]
+    per_layer = []
+    for l in range(layers):
+        if l == 0:
+            per_layer.append([w.ptrs[0] for w in base])
+            continue
+        ptrs = []
+        for w in base:
+            p = fakhip.alloc_call("fhip_malloc", w.nbytes)
+            fakhip.call("fhip_d2d", p, w.ptrs[0], w.nbytes)
+            ptrs.append(p)
+        per_layer.append(ptrs)
+    head = Weight("q4k", V, H, 60, 1)
+    xs = {k: Buf(k * 4, synth.activations(1, k, 70 + k)[0]) for k in (H, F)}
+    ys = {n: Buf(n * 4) for n in (H, KV, F, V)}
+    calls = []
+    for l in range(layers):
+        for (n, k), p in zip(layer_shapes, per_layer[l]):
+            calls.append(("fhip_q4k_matmul_f32",
+                          lambda i, p=p, n=n, k=k: (p, xs[k].ptr, ys[n].ptr, n, k, 1)))
+    calls.append(("fhip_q4k_matmul_f32",
+                  lambda i: (head.ptrs[0], xs[H].ptr, ys[V].ptr, V, H, 1)))
+    ms, per = time_calls(calls, steps, warmup, ev)
+    wbytes = layers * sum(q4k_bytes(n, k) for n, k in layer_shapes) + q4k_bytes(V, H)
+    abytes = layers * sum(4 * (n + k) for n, k in layer_shapes) + 4 * (V + H)
+    for l in range(1, layers):
+        for p in per_layer[l]:
+            fakhip.load().fhip_free(p)
+    for w in base + [head]:
+        w.free()
+    for b in list(xs.values()) + list(ys.values()):
+        b.free()
+    return {"layers": layers, "gemvs_per_token": len(calls), "weight_bytes": wbytes,
+            "ms_per_token": ms, "tok_per_s": 1e3 / ms,
+            "GBs": (wbytes + abytes) / (ms * 1e6),
+            "pct_hbm_peak": 100.0 * (wbytes + abytes) / (ms * 1e6) / HBM_PEAK_GBS,
+            "sum_of_call_ms": sum(per)}
+
+
+def cpu_baseline(ws, xs, ys, budget_s=10.0):
+    """The oracle (C restatement of q4kMatRowsRange, row-parallel like parForRange) timed on the
+    same C2 inputs on this host's cores; also reports the GPU result's error against it."""
+    import oracle  # the checker: used only in this leg
+    workers = min(os.cpu_count() or 1, 16)
+    reps, t0 = 0, time.perf_counter()
+    times = []
+    errs = []
+    while time.perf_counter() - t0 < budget_s or reps < 2:
+        ts = time.perf_counter()
+        outs = [oracle.q4k_matrows(w.raw, w.n, w.k, x, workers=workers) for w, (x, _) in zip(ws, xs)]
+        times.append(time.perf_counter() - ts)
+        reps += 1
+        if reps == 1:
+            for w, y, ref in zip(ws, ys, outs):
+                got = y.host()
+                errs.append(float(np.max(np.abs(got - ref)) / np.sqrt(np.mean(ref.astype(np.float64) ** 2))))
+        if reps >= 50:
+            break
+    med = float(np.median(times))
+    alg = sum(q4k_bytes(w.n, w.k) + 4 * (w.n + w.k) for w in ws)
+    return {"value": alg / med / 1e9, "unit": "GB/s", "cores": workers, "kind": "port",
+            "sample": f"full C2 pair (gate/up 3584->18944 + down 18944->3584, M=1), {reps} reps, "
+                      f"median {med * 1e3:.1f} ms",
+            "gpu_max_rel_err_vs_oracle": errs}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+              f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    info = fakhip.init()
+    print(f"[bench] device {info['name']} gfx{info['arch']} "
+          f"{info['total_mem'] / 2**30:.0f} GiB", file=sys.stderr, flush=True)
+    ev = Events()
+    c2, ws, xs, ys = bench_gemv_pair(args.steps, args.warmup, ev)
+    print(f"[bench] C2 pair {c2['ms_per_step'] * 1e3:.2f} us/step, per call "
+          f"{[round(u, 2) for u in c2['per_call_us']]} us", file=sys.stderr, flush=True)
+    alg_step = sum(c2["alg_bytes"])
+    value = alg_step / (c2["ms_per_step"] * 1e6)
+    # dominant kernel: the gate/up GEMV call (xprep + GEMV), timed per launch with HIP events
+    gate_gbs = c2["per_call_GBs"][0]
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(c2["ms_per_step"], 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded GGUF Q4_K blocks, N(0,1) activations)",
+        "config": {"workload": "Q4_K decode GEMV M=1, Qwen2.5-7B FFN: gate/up K=3584 N=18944 + "
+                               "down K=18944 N=3584", "M": 1,
+                   "weight_copies_rotated": c2["copies"]},
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 1),
+        "roofline": {"bound": "hbm", "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "fhip_q4k_matmul_f32 gate/up (gemv_xprep + q4k_gemv_kernel<1>)",
+                     "alg_bytes_per_launch": c2["alg_bytes"][0],
+                     "launch_us": round(c2["per_call_us"][0], 3)},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(ws, xs, ys)
+    for w in ws:
+        w.free()
+    if not args.quick:
+        wl = {}
+        steps = max(10, args.steps // 4)
+        wl["c1_q8_0_gemv"] = bench_q8_0(args.steps, args.warmup, ev)
+        wl["c3_prefill_gemm"] = [bench_gemm(M, steps, 3, ev) for M in (128, 512, 2048)]
+        wl["c4_decode_stack"] = bench_decode_stack(max(5, args.steps // 20), 2, ev)
+        wl["c5_small_m"] = bench_small_m(steps, 3, ev)
+        line["workloads"] = wl
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,322 @@
+"""Host-side mirror of fak's compute HAL seam for the quantized matmul path.
+
+The Go engine selects a device through ``compute.Backend`` (internal/compute/compute.go:318-347)
+and a registry (``Register``/``Lookup``/``Pick``/``Default``, compute.go:464-519). The CUDA
+tenant (internal/compute/cuda.go) implements Upload / Read / Free / MatMul / BatchedMatMul over
+a flat C ABI. This module restates that contract for the ROCm backend over the fakhip C ABI, with
+the same names, argument meaning and failure behaviour (a Go panic becomes a Python exception):
+
+* ``Tensor`` carries Dtype, Layout, Shape, QuantSpec and an opaque buffer (compute.go:168-175).
+* ``RocmBackend.Upload`` copies raw GGUF Q4_K bytes (``NewQ4K``, internal/compute/quant_q4k.go:
+  37-44) or raw GGUF Q8_0 blocks resident in the tiled layout, caching by host buffer with an
+  element-count guard (cuda.go:690-704, 803-822); F32 activations upload verbatim.
+* ``MatMul(w, x)`` is y = x @ W^T (w [out,in], x [in] -> y [out]) and ``BatchedMatMul(w, X, P)``
+  is the [P,in] -> [P,out] prefill GEMM, dispatched on ``w.Dtype`` (cuda.go:956-1035), each with
+  the reference's shape post-condition.
+* The backend class is Approx (harness-enforced, compute.go:212-217, 525).
+
+Only the quantized weight path lives here; RMSNorm/RoPE/attention and the f32/f16 GEMMs are
+outside this backend's scope and raise NotImplementedError.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+import enum
+from typing import Optional
+
+import numpy as np
+
+from . import fakhip
+
+
+class Dtype(enum.IntEnum):
+    """internal/compute/compute.go:53-64 (same order and values)."""
+    F32 = 0
+    F16 = 1
+    BF16 = 2
+    Q8_0 = 3
+    I8 = 4
+    I4 = 5
+    FP8 = 6
+    Q4_K = 7
+
+    def __str__(self) -> str:  # compute.go:80-101
+        return {0: "f32", 1: "f16", 2: "bf16", 3: "q8_0", 4: "i8", 5: "i4", 6: "fp8",
+                7: "q4_k"}.get(int(self), "dtype?")
+
+
+class Layout(enum.IntEnum):
+    """internal/compute/compute.go:113-117."""
+    RowMajor = 0
+    ColMajor = 1
+    Tiled = 2
+
+
+class CorrectnessClass(enum.IntEnum):
+    """internal/compute/compute.go:212-217."""
+    Reference = 0
+    Approx = 1
+
+
+@dataclasses.dataclass
+class QuantSpec:
+    """internal/compute/compute.go:130-141."""
+    Block: int = 0
+    Axis: int = 0
+    Bits: int = 0
+    Symmetric: bool = False
+    Scale: Optional[np.ndarray] = None
+
+
+@dataclasses.dataclass
+class Caps:
+    """internal/compute/compute.go:234-256 (the fields this backend sets)."""
+    Async: bool = False
+    FusedAttn: bool = False
+    FusedFFN: bool = False
+    GraphCompile: bool = False
+    UploadDtype: bool = False
+    DeviceMemory: bool = False
+    Collective: bool = False
+    CapacityProbe: bool = False
+
+
+class HostBuf:
+    """A host-resident buffer (the reference's HostBuffer: F32() / I8() views)."""
+
+    def __init__(self, f32: Optional[np.ndarray] = None, i8: Optional[np.ndarray] = None):
+        self.f32 = f32
+        self.i8 = i8
+
+    def Ready(self) -> bool:
+        return True
+
+
+class DevBuf:
+    """A device-resident buffer: pointer into the fakhip pool + byte length."""
+
+    def __init__(self, ptr: int, nbytes: int, host_key=None):
+        self.ptr = ptr
+        self.nbytes = nbytes
+        self.host_key = host_key
+
+    def Ready(self) -> bool:
+        return True
+
+
+@dataclasses.dataclass
+class Tensor:
+    """internal/compute/compute.go:168-175."""
+    Dtype: Dtype
+    Layout: Layout
+    Shape: list
+    Quant: Optional[QuantSpec]
+    buf: object
+    be: object = None
+
+    def Numel(self) -> int:
+        n = 1
+        for d in self.Shape:
+            n *= d
+        return n
+
+
+def NewF32(be, shape, data) -> Tensor:
+    """internal/compute/cpuref.go:47-49."""
+    return Tensor(Dtype.F32, Layout.RowMajor, list(shape), None,
+                  HostBuf(f32=np.ascontiguousarray(data, np.float32).reshape(-1)), be)
+
+
+def NewQ4K(be, shape, raw) -> Tensor:
+    """Raw GGUF Q4_K bytes as a host tensor (internal/compute/quant_q4k.go:37-44)."""
+    raw = np.ascontiguousarray(raw, np.uint8).reshape(-1)
+    return Tensor(Dtype.Q4_K, Layout.RowMajor, list(shape),
+                  QuantSpec(Block=256, Axis=2, Bits=4, Symmetric=False), HostBuf(i8=raw), be)
+
+
+def NewQ8_0GGUF(be, shape, raw) -> Tensor:
+    """Raw GGUF Q8_0 blocks (f16 d + 32 int8) as a host Q8_0 tensor. The scale is recorded per
+    block as f32 (the exact widening of the stored f16), so the tensor carries the same values as
+    the reference's resident kqw Q8_0 weight (internal/model/quant_kquant.go:237-248)."""
+    raw = np.ascontiguousarray(raw, np.uint8).reshape(-1)
+    out, in_ = shape
+    blk = raw.reshape(out * (in_ // 32), 34)
+    scale = blk[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1)
+    return Tensor(Dtype.Q8_0, Layout.RowMajor, list(shape),
+                  QuantSpec(Block=32, Axis=2, Bits=8, Symmetric=True, Scale=scale),
+                  HostBuf(i8=raw), be)
+
+
+class RocmBackend:
+    """The ROCm (gfx950) Approx backend behind the compute.Backend seam."""
+
+    def __init__(self):
+        self.info = fakhip.init()
+        self._upload_cache: dict = {}
+
+    # ---- identity (compute.go:319-322) ----
+    def Name(self) -> str:
+        return "rocm"
+
+    def Tier(self) -> str:
+        return "gfx950"
+
+    def Class(self) -> CorrectnessClass:
+        return CorrectnessClass.Approx
+
+    def Caps(self) -> Caps:
+        return Caps(Async=True, UploadDtype=True, DeviceMemory=True, CapacityProbe=True)
+
+    # ---- residency ----
+    def Upload(self, t: Tensor, as_: Dtype = Dtype.F32) -> Tensor:
+        if not isinstance(t.buf, HostBuf):
+            raise TypeError("compute: rocm Upload expects host data")
+        if t.Dtype == Dtype.Q4_K:
+            return self._upload_quant(t, "fhip_q4k_upload", 256, 144)
+        if t.Dtype == Dtype.Q8_0:
+            return self._upload_quant(t, "fhip_q8_0_upload", 32, 34)
+        if t.Dtype != Dtype.F32:
+            raise TypeError(f"compute: rocm Upload supports F32 host data or raw Q4_K / Q8_0 "
+                            f"blocks (got {t.Dtype})")
+        f = t.buf.f32
+        n = f.size * 4
+        ptr = fakhip.alloc_call("fhip_malloc", max(n, 4))
+        if n:
+            fakhip.call("fhip_h2d", ptr, f.ctypes.data, n)
+        return Tensor(Dtype.F32, Layout.RowMajor, list(t.Shape), None, DevBuf(ptr, n), self)
+
+    def _upload_quant(self, t: Tensor, fn: str, block: int, block_bytes: int) -> Tensor:
+        if len(t.Shape) != 2:
+            raise ValueError(f"compute: rocm Upload({t.Dtype}) expects a 2-D [out,in] weight")
+        out, in_ = t.Shape
+        raw = t.buf.i8
+        if in_ % block:
+            raise ValueError(f"compute: {t.Dtype} reduction dim {in_} not a multiple of {block}")
+        want = out * (in_ // block) * block_bytes
+        if raw.size != want:
+            raise ValueError(f"compute: {t.Dtype} payload size {raw.size} != {want}")
+        key = (raw.ctypes.data, int(t.Dtype))
+        cached = self._upload_cache.get(key)
+        if cached is not None and cached.Numel() == t.Numel():
+            return cached
+        ptr = fakhip.alloc_call(fn, raw.ctypes.data, out, in_)
+        res = Tensor(t.Dtype, Layout.Tiled, [out, in_], t.Quant, DevBuf(ptr, want, key), self)
+        self._upload_cache[key] = res
+        return res
+
+    def Host(self, t: Tensor):
+        return None, False
+
+    def Read(self, t: Tensor) -> np.ndarray:
+        """Device -> host f32 (the host fence)."""
+        if t.Dtype != Dtype.F32:
+            raise TypeError("compute: rocm Read supports F32 tensors")
+        out = np.empty(t.Numel(), np.float32)
+        if out.size:
+            fakhip.call("fhip_d2h", out.ctypes.data, t.buf.ptr, out.size * 4)
+        return out
+
+    def Free(self, t: Tensor) -> None:
+        if isinstance(t.buf, DevBuf) and t.buf.ptr:
+            if t.buf.host_key is not None:
+                self._upload_cache.pop(t.buf.host_key, None)
+            fakhip.load().fhip_free(t.buf.ptr)
+            t.buf.ptr = 0
+
+    # ---- the quantized matmul family ----
+    def _dev_out(self, shape) -> Tensor:
+        n = int(np.prod(shape)) * 4
+        ptr = fakhip.alloc_call("fhip_malloc", max(n, 4))
+        return Tensor(Dtype.F32, Layout.RowMajor, list(shape), None, DevBuf(ptr, n), self)
+
+    def _matmul(self, w: Tensor, X: Tensor, P: int, shape) -> Tensor:
+        out, in_ = w.Shape
+        if X.Dtype != Dtype.F32 or not isinstance(X.buf, DevBuf):
+            raise TypeError("compute: rocm MatMul expects a device-resident F32 activation")
+        if X.Numel() != P * in_:
+            raise ValueError(f"compute: rocm MatMul activation has {X.Numel()} elements, want "
+                             f"{P}x{in_}")
+        y = self._dev_out(shape)
+        if w.Dtype == Dtype.Q4_K:
+            fakhip.call("fhip_q4k_matmul_f32", w.buf.ptr, X.buf.ptr, y.buf.ptr, out, in_, P)
+        elif w.Dtype == Dtype.Q8_0:
+            fakhip.call("fhip_q8_0_matmul_f32", w.buf.ptr, X.buf.ptr, y.buf.ptr, out, in_, P)
+        else:
+            raise NotImplementedError(f"compute: rocm MatMul supports Q4_K / Q8_0 weights "
+                                      f"(got {w.Dtype})")
+        return y
+
+    def MatMul(self, w: Tensor, x: Tensor) -> Tensor:
+        out, in_ = w.Shape
+        y = self._matmul(w, x, 1, [out])
+        if y.Numel() != out:  # cuda.go:989-993
+            raise RuntimeError(f"compute: rocm MatMul {w.Dtype} out={out} in={in_} produced "
+                               f"{y.Numel()} rows")
+        return y
+
+    def BatchedMatMul(self, w: Tensor, X: Tensor, P: int) -> Tensor:
+        out, in_ = w.Shape
+        y = self._matmul(w, X, P, [P, out])
+        if y.Numel() != P * out:  # cuda.go:1029-1033
+            raise RuntimeError(f"compute: rocm BatchedMatMul {w.Dtype} out={out} in={in_} P={P} "
+                               f"produced {y.Numel()} want {P * out}")
+        return y
+
+    # The rest of the Backend interface belongs to other kernels.
+    def RMSNorm(self, *a):
+        raise NotImplementedError("compute: rocm backend implements the quantized matmul only")
+
+    RoPE = SwiGLU = AddInPlace = AddBias = Attention = Argmax = NewKV = RMSNorm
+
+
+# ---- registry (internal/compute/compute.go:464-519) ----
+_registry: list = []
+
+
+def Register(b) -> None:
+    for i, e in enumerate(_registry):
+        if e.Name() == b.Name():
+            _registry[i] = b
+            return
+    _registry.append(b)
+
+
+def Registered() -> list:
+    return [b.Name() for b in _registry]
+
+
+def Lookup(name: str):
+    for b in _registry:
+        if b.Name() == name:
+            return b, True
+    return None, False
+
+
+def Pick(name: str):
+    if name:
+        b, ok = Lookup(name)
+        if ok:
+            return b
+    return Default()
+
+
+def Default():
+    for b in _registry:
+        if b.Class() == CorrectnessClass.Reference:
+            return b
+    return _registry[0] if _registry else None
+
+
+def RequireReference(b) -> bool:
+    return b is not None and b.Class() == CorrectnessClass.Reference
+
+
+def register_rocm() -> Optional[RocmBackend]:
+    """The init() of cuda.go:212-232: register "rocm" when a gfx950 device is reachable."""
+    try:
+        be = RocmBackend()
+    except fakhip.FakHipError:
+        return None
+    Register(be)
+    return be

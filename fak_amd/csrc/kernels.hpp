@@ -1,0 +1,32 @@
+// kernels.hpp — device helpers and launchers shared by the Q4_K / Q8_0 matmul kernels.
+#pragma once
+
+#include "common.hpp"
+#include "tiled.hpp"
+
+namespace fhip {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// The order in which a lane's 8 K-elements sit in its MFMA operand: element j holds the value
+// at K offset kPerm[j] within the lane's 8-run. It is the order the nibble unpack produces
+// (bytes 0,2 then 1,3 of each dword); the activation operands are built in the same order, so
+// every product pairs a weight with its own activation.
+__host__ __device__ constexpr int perm8(int j) { return (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1); }
+
+// Large-M activation operands for the GEMM: X [M][K] f32 -> f16 tiles in MFMA A-operand order:
+//   xa[((mt * (K/32) + s) * 64 + l)] = 8 f16 values f16(x[16 mt + (l & 15)][32 s + 8 (l >> 4)
+//   + perm8(j)]), rows past M are zero. Bytes: roundup(M,16) * K * 2.
+inline size_t gemm_xa_bytes(int M, int K) { return (size_t)ceil_div(M, 16) * 16 * K * 2; }
+int launch_gemm_xprep(const float *X, int M, int K, void *xa);
+
+int q4k_gemv(const void *W, const float *X, float *Y, int N, int K, int M);
+int q4k_gemm(const void *W, const float *X, float *Y, int N, int K, int M);
+int q8_0_gemv(const void *W, const float *X, float *Y, int N, int K, int M);
+
+// Read an integer tuning override from the environment (0 when unset).
+int env_int(const char *name);
+
+}  // namespace fhip

@@ -1,0 +1,70 @@
+"""Single-shape matmul microbenchmark, in the style of fak's cmd/q8kernel: one weight shape, M
+tokens, a number of repetitions, median-free plain timing with HIP events, and a one-line report.
+Used as the target program for rocprofv3 runs (kernel trace, counters) on one shape.
+
+    python -m fak_amd.q4kbench --n 18944 --k 3584 --m 1 --reps 20 [--q8]
+
+Weights rotate over enough distinct device copies (> 256 MB) that the Infinity Cache cannot
+serve them.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+
+from . import fakhip, synth
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--n", type=int, required=True, help="output rows")
+    ap.add_argument("--k", type=int, required=True, help="reduction dim")
+    ap.add_argument("--m", type=int, default=1, help="tokens")
+    ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--q8", action="store_true", help="Q8_0 weights instead of Q4_K")
+    ap.add_argument("--seed", type=int, default=1)
+    a = ap.parse_args()
+    fakhip.init()
+    lib = fakhip.load()
+    if a.q8:
+        raw = synth.q8_0_weights(a.n, a.k, a.seed)
+        up, mm, nbytes = "fhip_q8_0_upload", "fhip_q8_0_matmul_f32", lib.fhip_q8_0_packed_bytes(a.n, a.k)
+        alg = a.n * (a.k // 32) * 34
+    else:
+        raw = synth.q4k_weights(a.n, a.k, a.seed)
+        up, mm, nbytes = "fhip_q4k_upload", "fhip_q4k_matmul_f32", lib.fhip_q4k_packed_bytes(a.n, a.k)
+        alg = a.n * (a.k // 256) * 144
+    p0 = fakhip.alloc_call(up, raw.ctypes.data, a.n, a.k)
+    ptrs = [p0]
+    for _ in range(max(1, (300 << 20) // nbytes)):
+        p = fakhip.alloc_call("fhip_malloc", nbytes)
+        fakhip.call("fhip_d2d", p, p0, nbytes)
+        ptrs.append(p)
+    X = synth.activations(a.m, a.k, a.seed + 1)
+    dx = fakhip.alloc_call("fhip_malloc", X.nbytes)
+    fakhip.call("fhip_h2d", dx, X.ctypes.data, X.nbytes)
+    dy = fakhip.alloc_call("fhip_malloc", a.m * a.n * 4)
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    fakhip.call("fhip_event_create", C.byref(e0))
+    fakhip.call("fhip_event_create", C.byref(e1))
+    fakhip.call(mm, ptrs[0], dx, dy, a.n, a.k, a.m)
+    fakhip.call("fhip_sync")
+    fakhip.call("fhip_event_record", e0)
+    for i in range(a.reps):
+        fakhip.call(mm, ptrs[i % len(ptrs)], dx, dy, a.n, a.k, a.m)
+    fakhip.call("fhip_event_record", e1)
+    ms = C.c_float()
+    fakhip.call("fhip_event_elapsed_ms", e0, e1, C.byref(ms))
+    us = ms.value * 1e3 / a.reps
+    bytes_ = alg + 4 * a.m * (a.n + a.k)
+    print(json.dumps({"n": a.n, "k": a.k, "m": a.m, "q8_0": a.q8, "reps": a.reps,
+                      "us_per_call": round(us, 3), "GBs": round(bytes_ / us / 1e3, 1),
+                      "TFLOPs": round(2.0 * a.m * a.n * a.k / us / 1e6, 2),
+                      "weight_copies": len(ptrs)}), flush=True)
+    for p in ptrs + [dx, dy]:
+        lib.fhip_free(p)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,125 @@
+/* fakhip.h — the flat C ABI of the MI355X (gfx950) HIP backend for fak's GGUF Q4_K / Q8_0
+ * dequantize-and-multiply hot path.
+ *
+ * It is the ROCm twin of the CUDA tenant's flat ABI (internal/compute/cuda_backend.h): a host
+ * binding (the Go cgo wrapper, a ctypes stub, a C++ harness) owns shapes, residency policy and
+ * tensor types; this header carries only device pointers, sizes and integer status codes. It
+ * includes nothing but <stddef.h>/<stdint.h>, so a plain host compiler (cgo's) can parse it.
+ *
+ * Conventions
+ *   - Every entry that can fail returns int: 0 = ok; FHIP_EINVAL (-1) = bad argument (shape,
+ *     null pointer, unsupported size); FHIP_ENODEV (-2) = no usable gfx950 device;
+ *     FHIP_ENOMEM (-3) = allocation failed; 1000 + hipError_t = a HIP runtime error.
+ *     fhip_last_error() returns a human-readable message for the last failure on the calling
+ *     thread. (The CUDA ABI returned void and printed; cuda_backend.h:227-237 already used
+ *     int codes for its NCCL entries, which this ABI adopts throughout.)
+ *   - Pointers named d* are device pointers, h* are host pointers.
+ *   - All launches and async copies go to the library's current stream (fhip_set_stream; the
+ *     null/default stream until set). Calls are NOT thread-safe: the host serializes them,
+ *     exactly as the CUDA tenant's single cudaMu mutex does (internal/compute/cuda.go:40-43).
+ *   - Weights are uploaded once in a backend-private "tiled" layout (fhip_q4k_repack /
+ *     fhip_q8_0_repack). The layout is a lossless byte permutation of the GGUF blocks (the
+ *     exact inverse is fhip_*_unpack); it costs the same 144 B per 256 Q4_K weights and 34 B per
+ *     32 Q8_0 weights, padded only to a multiple of 16 output rows.
+ */
+#ifndef FAK_HIP_BACKEND_H
+#define FAK_HIP_BACKEND_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FHIP_OK 0
+#define FHIP_EINVAL (-1)
+#define FHIP_ENODEV (-2)
+#define FHIP_ENOMEM (-3)
+
+/* ---- runtime ----------------------------------------------------------------------------- */
+
+/* Select device 0, verify it is gfx950, and report its name (up to namelen-1 chars), gfx
+ * arch number (e.g. 950) and total memory. Idempotent. Replaces fcuda_init
+ * (internal/compute/cuda_backend.h:25). Non-zero when no gfx950 device is reachable. */
+int fhip_init(char *name, int namelen, int *arch, size_t *total_mem);
+/* Replaces fcuda_mem_info (cuda_backend.h:28). */
+int fhip_mem_info(size_t *free_mem, size_t *total_mem);
+/* Message for the last failing call on this thread ("" if none). */
+const char *fhip_last_error(void);
+
+/* Device memory from a size-bucketed pool: fhip_free returns the block to the pool, not to the
+ * driver (fcuda_malloc / fcuda_free / fcuda_trim_pool_large, cuda_backend.h:31-34).
+ * fhip_malloc returns NULL on failure (reason via fhip_last_error). */
+void *fhip_malloc(size_t bytes);
+void fhip_free(void *d);
+/* Release pooled (free) blocks until at most max_keep_bytes stay cached. */
+void fhip_trim_pool(size_t max_keep_bytes);
+/* Synchronous copies (fcuda_h2d / fcuda_d2h / fcuda_d2d, cuda_backend.h:35-37) and a device
+ * synchronize (fcuda_sync, :38). */
+int fhip_h2d(void *d, const void *h, size_t bytes);
+int fhip_d2h(void *h, const void *d, size_t bytes);
+int fhip_d2d(void *dst, const void *src, size_t bytes);
+int fhip_sync(void);
+/* Asynchronous copies on the current stream (no counterpart in the CUDA ABI, which ran
+ * every copy synchronously on its single g_stream). */
+int fhip_h2d_async(void *d, const void *h, size_t bytes);
+int fhip_d2h_async(void *h, const void *d, size_t bytes);
+int fhip_memset_async(void *d, int value, size_t bytes);
+
+/* Streams and events (the CUDA tenant has one global g_stream, cuda_kernels.cu:28-32; this
+ * backend exposes the stream as a handle so a host can overlap work or capture graphs).
+ * Streams are created at the default priority. */
+int fhip_stream_create(void **stream);
+int fhip_stream_destroy(void *stream);
+/* Make `stream` (NULL = the default stream) the target of every later launch and async copy. */
+int fhip_set_stream(void *stream);
+int fhip_stream_sync(void *stream);
+int fhip_event_create(void **event);
+int fhip_event_destroy(void *event);
+/* Record on the current stream. */
+int fhip_event_record(void *event);
+/* Wait for `end`, then report the elapsed milliseconds between two recorded events. */
+int fhip_event_elapsed_ms(void *start, void *end, float *ms);
+
+/* ---- Q4_K (256-weight super-blocks of 144 B: f16 d, f16 dmin, 12 B of 6-bit scales/mins,
+ *      128 B of nibbles; internal/model/quant_q4k.go:22-26) ------------------------------- */
+
+/* Bytes of the tiled layout for an [out, in] weight (in % 256 == 0). */
+size_t fhip_q4k_packed_bytes(int out, int in);
+/* dPacked <- tiled layout of the raw row-major GGUF bytes dRaw (out*(in/256)*144 bytes). */
+int fhip_q4k_repack(void *dPacked, const uint8_t *dRaw, int out, int in);
+/* dRaw <- raw GGUF bytes recovered from the tiled layout (exact inverse of fhip_q4k_repack). */
+int fhip_q4k_unpack(uint8_t *dRaw, const void *dPacked, int out, int in);
+/* dW[out*in] <- f32 dequantized weights, bit-identical to q4kDequantSuperBlock
+ * (internal/model/quant_q4k.go:90-111) for every input, NaN payloads included. Test hook. */
+int fhip_q4k_dequant_f32(float *dW, const void *dPacked, int out, int in);
+/* Allocate (pool) a tiled Q4_K weight and fill it from host raw GGUF bytes: the upload path
+ * of uploadQ4K (internal/compute/cuda.go:803-822). Returns NULL on failure. Free with
+ * fhip_free. */
+void *fhip_q4k_upload(const uint8_t *hRaw, int out, int in);
+/* Y[P,out] = X[P,in] @ W[out,in]^T with W a tiled Q4_K weight, X and Y row-major f32 — the
+ * replacement for fcuda_q4k_matmul_f32 (internal/compute/cuda_backend.h:120), which took the
+ * raw bytes; this one takes the tiled buffer fhip_q4k_upload / fhip_q4k_repack produced.
+ * P <= 16 runs the small-M GEMV (decode / speculative verify); larger P runs the MFMA GEMM.
+ * Error bound vs the f32 reference: GEMV max|dY|/RMS(Y) <= 1e-3, GEMM <= 1e-2. */
+int fhip_q4k_matmul_f32(const void *dPacked, const float *dX, float *dY, int out, int in,
+                        int P);
+
+/* ---- Q8_0 (32-weight blocks of 34 B: f16 d + 32 int8; internal/ggufload/gguf.go:24) ----- */
+
+size_t fhip_q8_0_packed_bytes(int out, int in);
+int fhip_q8_0_repack(void *dPacked, const uint8_t *dRaw, int out, int in);
+int fhip_q8_0_unpack(uint8_t *dRaw, const void *dPacked, int out, int in);
+/* bit-identical to q8_0DequantBlock (internal/model/quant_iquant.go:14-19). Test hook. */
+int fhip_q8_0_dequant_f32(float *dW, const void *dPacked, int out, int in);
+void *fhip_q8_0_upload(const uint8_t *hRaw, int out, int in);
+/* Y[P,out] = X[P,in] @ W^T with W a tiled Q8_0 weight and f32 activations: the device form of
+ * kQuantMatRowsRange(kind Q8_0) (internal/model/quant_kquant.go:210-232). f32 accumulate,
+ * max|dY|/RMS(Y) <= 1e-3. */
+int fhip_q8_0_matmul_f32(const void *dPacked, const float *dX, float *dY, int out, int in,
+                         int P);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

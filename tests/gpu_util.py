@@ -1,0 +1,77 @@
+"""Small helpers for GPU tests: numpy <-> device buffers through the fakhip C ABI only."""
+from __future__ import annotations
+
+import numpy as np
+
+from fak_amd import fakhip
+
+
+class Dev:
+    """A device allocation from the fakhip pool, freed on close."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        self.ptr = fakhip.alloc_call("fhip_malloc", max(self.nbytes, 16))
+
+    @classmethod
+    def from_host(cls, a: np.ndarray) -> "Dev":
+        a = np.ascontiguousarray(a)
+        d = cls(a.nbytes)
+        if a.nbytes:
+            fakhip.call("fhip_h2d", d.ptr, a.ctypes.data, a.nbytes)
+        return d
+
+    def to_host(self, dtype, count: int | None = None) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        n = self.nbytes // dtype.itemsize if count is None else count
+        out = np.empty(n, dtype)
+        if out.nbytes:
+            fakhip.call("fhip_d2h", out.ctypes.data, self.ptr, out.nbytes)
+        return out
+
+    def close(self):
+        if self.ptr:
+            fakhip.load().fhip_free(self.ptr)
+            self.ptr = 0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+
+def rel_err(got: np.ndarray, ref: np.ndarray) -> float:
+    """The reference's metric: max|got - ref| / RMS(ref) (internal/model/quant_q4k_test.go:140-158)."""
+    ref = np.asarray(ref, np.float64)
+    rms = np.sqrt(np.mean(ref * ref))
+    return float(np.max(np.abs(np.asarray(got, np.float64) - ref)) / rms)
+
+
+def cosine(a, b) -> float:
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def q4k_matmul(raw: np.ndarray, out: int, in_: int, X: np.ndarray, P: int) -> np.ndarray:
+    """Upload raw Q4_K, run fhip_q4k_matmul_f32 on X[P, in], return Y[P, out]."""
+    lib = fakhip.load()
+    w = fakhip.alloc_call("fhip_q4k_upload", np.ascontiguousarray(raw).ctypes.data, out, in_)
+    try:
+        with Dev.from_host(np.ascontiguousarray(X, np.float32)) as dx, Dev(P * out * 4) as dy:
+            fakhip.call("fhip_q4k_matmul_f32", w, dx.ptr, dy.ptr, out, in_, P)
+            return dy.to_host(np.float32).reshape(P, out)
+    finally:
+        lib.fhip_free(w)
+
+
+def q8_0_matmul(raw: np.ndarray, out: int, in_: int, X: np.ndarray, P: int) -> np.ndarray:
+    lib = fakhip.load()
+    w = fakhip.alloc_call("fhip_q8_0_upload", np.ascontiguousarray(raw).ctypes.data, out, in_)
+    try:
+        with Dev.from_host(np.ascontiguousarray(X, np.float32)) as dx, Dev(P * out * 4) as dy:
+            fakhip.call("fhip_q8_0_matmul_f32", w, dx.ptr, dy.ptr, out, in_, P)
+            return dy.to_host(np.float32).reshape(P, out)
+    finally:
+        lib.fhip_free(w)
