@@ -28,18 +28,40 @@ CXXFLAGS = [
 ]
 
 
+RESOURCE_REMARK = "kernel-resource-usage"
+
+
+def scratch_kernels(remarks: str) -> list[tuple[str, int]]:
+    """(kernel, bytes/lane) for every kernel whose resource-usage remark reports scratch."""
+    out, name = [], None
+    for line in remarks.splitlines():
+        if "Function Name:" in line:
+            name = line.split("Function Name:")[1].split("[")[0].strip()
+        elif "ScratchSize [bytes/lane]:" in line and name:
+            n = int(line.split("ScratchSize [bytes/lane]:")[1].split("[")[0])
+            if n:
+                out.append((name, n))
+    return out
+
+
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *CXXFLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *CXXFLAGS, f"-Rpass-analysis={RESOURCE_REMARK}", "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
-    msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
-                     if "packed-fp32-ops" not in l and l.strip())
+    out = r.stdout + r.stderr
+    msgs = "\n".join(l for l in out.splitlines()
+                     if "packed-fp32-ops" not in l and RESOURCE_REMARK not in l and l.strip())
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{msgs}")
     if msgs and verbose:
         print(msgs, flush=True)
+    # Register spills to scratch memory cost these bandwidth-bound kernels far more than they
+    # save; every kernel must fit its registers.
+    spills = scratch_kernels(out)
+    if spills:
+        raise RuntimeError(f"{src}: kernels use scratch memory (register spills): {spills}")
     return obj
 
 

@@ -23,6 +23,7 @@ inline size_t gemm_xa_bytes(int M, int K) { return (size_t)ceil_div(M, 16) * 16 
 int launch_gemm_xprep(const float *X, int M, int K, void *xa);
 
 int q4k_gemv(const void *W, const float *X, float *Y, int N, int K, int M);
+int q4k_gemv_wide(const void *W, const float *X, float *Y, int N, int K, int M);
 int q4k_gemm(const void *W, const float *X, float *Y, int N, int K, int M);
 int q8_0_gemv(const void *W, const float *X, float *Y, int N, int K, int M);
 

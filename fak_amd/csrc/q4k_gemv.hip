@@ -1,83 +1,223 @@
-// q4k_gemv.hip — small-M (1..16 tokens) Q4_K matmul: decode GEMV and speculative verify.
+// q4k_gemv.hip — small-M (1..4 tokens) Q4_K matmul: the decode GEMV run for every generated
+// token, and narrow speculative-verify batches. Wider batches (5..16) use q4k_gemv_wide.hip.
 //
 // Computes Y[t][o] = sum_k W[o][k] * X[t][k] with W the dequantized Q4_K weight
-// (w = d*sc*n - dmin*m per 32-weight sub-block, internal/model/quant_q4k.go:90-111) without
-// ever materialising w. Per sub-block s of row o and token t the sum factors as
-//   sum_k w x = d*sc_s * sum_k n_k x_k  -  dmin*m_s * S_s,      S_s = sum_k x_k
-// and the inner integer-weight dot runs on a 16x16x32 f16 MFMA:
-//   * weight operand: the 4-bit codes themselves, exact in f16. A nibble pair becomes two f16
-//     values with one and-or: (q & 0x000F000F) | 0x64006400 = (1024 + n0, 1024 + n2) (the high
-//     nibbles, masked in place, give 1024 + 16 n). The 1024 * S_s this adds is subtracted after
-//     the MFMA.
-//   * activation operand: X split into f16 hi and lo rows (gemv_common.hpp), so each token uses
-//     two of the MFMA's 16 rows and the products carry ~22 bits of the activation.
-// After each MFMA the f32 result is scaled per (row, sub-block) on the VALU.
+// (w = d*sc_s*n - dmin*m_s for sub-block s, internal/model/quant_q4k.go:90-111) without ever
+// materialising w. Per sub-block s of row o and token t the sum factors as
+//   sum_k w x = d * sc_s * sum_k n_k x_k  -  dmin * m_s * S_s,        S_s = sum_k x_k,
+// and the integer-weight dot sum_k n_k x_k runs on the int8 MFMA v_mfma_i32_16x16x64_i8:
+//   * weight operand: the 4-bit codes n (0..15) are int8 values as they stand; a dword of 8
+//     nibbles becomes two int8x4 words, `q & 0x0F0F0F0F` and `(q >> 4) & 0x0F0F0F0F`.
+//   * activation operand: every 32-value sub-block of a token is quantized to two int8 digits,
+//     x ~= e * (q1 + q2 / 256) = e * T / 256 with e the smallest power of two >= max|x| / 127
+//     and T = rint(256 x / e). The error is at most e / 512 per value (< 3.1e-5 of the block's
+//     largest magnitude), integer activations are exact, and the int32 products of both digits
+//     are exact. S_s is the f32 sum of the unquantized values.
 //
-// Work split. A workgroup owns TW 16-row tiles over the whole K; each tile is worked by KW
-// waves, each on a contiguous part of the super-blocks, and the KW partials are summed through
-// LDS in part order (deterministic, no cross-workgroup traffic). Every wave streams its tiled
-// weight records (tiled.hpp) exactly once with three coalesced 16-byte loads per lane per
-// 2304-byte record and keeps the next record in flight while it computes the current one.
+// Accumulator layout. One MFMA covers one 32-byte chunk c of a row's nibbles (sub-block 2c in
+// the low nibbles, 2c + 1 in the high nibbles) for the 16 rows of a tile. Its 16 operand rows
+// stand for (sub-block, token, digit) triples, so the four chunks of a super-block accumulate
+// into the SAME result: each lane loads its activation digits only into the operand of the MFMA
+// whose sub-block owns the lane's row (an exec-masked LDS read) and the other operands keep
+// zeros in that lane. For one token the 16 rows are the 8 sub-blocks x 2 digits, every result
+// lane is useful, and result lane group g holds sub-blocks g and g + 4 of the 16 output rows.
+// Two tokens use two results (sub-blocks 0-3, 4-7), four tokens one result per chunk.
 //
-// Activation operands: with LX the workgroup stages them for all of K into LDS itself (decode:
-// one launch per matmul); otherwise a separate gemv_xprep_kernel writes them to global memory
-// (used when M*K is too large for LDS) and the waves prefetch them with the weights.
+// Work split: a workgroup owns TW 16-row tiles, each worked by KW waves on contiguous parts of
+// the super-blocks. Every wave first puts its first PF weight records in flight, then the
+// whole workgroup quantizes the activations of all of K once into LDS for its TW tiles (when
+// that does not fit, gemv_i8_prep_kernel writes them to global memory once). Each wave streams
+// its tiled weight records (tiled.hpp) exactly once with three 16-byte loads per lane, keeping
+// PF in flight; the KW partials of a tile are summed through LDS in part order
+// (deterministic).
 #include "gemv_common.hpp"
 
 namespace fhip {
 namespace {
 
-// gfx9 VOP3 instructions cannot encode literal constants, so (q & mask) | magic with literal
-// operands compiles to two instructions. Holding the constants in registers (opaque to constant
-// folding) lets each nibble pair become one v_and_or_b32.
-__device__ __forceinline__ uint32_t in_reg(uint32_t x) {
-  asm volatile("" : "+v"(x));
-  return x;
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// ---- Activation operand layout for MP (1, 2, 4) token rows --------------------------------
+// Per super-block: MP result blocks of 16 rows x 4 lane groups x 16 bytes (entry index
+// ((bl * MP + blk) * 16 + row) * 4 + g), then per (sub-block, token) a float2 {e, S}.
+// Row `row` of block `blk` holds digit k of token t for sub-block sig (positions 8g..8g+7 of
+// the sub-block in bytes 0-7 when sig is even, bytes 8-15 when odd; the other half is zero).
+template <int MP>
+__host__ __device__ constexpr int blk_of(int sig) {
+  return MP == 1 ? 0 : MP == 2 ? sig >> 2 : sig >> 1;
+}
+template <int MP>
+__host__ __device__ constexpr int row_of(int sig, int t, int k) {
+  return MP == 1 ? 4 * (sig & 3) + 2 * (sig >> 2) + k
+       : MP == 2 ? 4 * (sig & 3) + 2 * t + k
+                 : 8 * (sig & 1) + 2 * t + k;
+}
+// Inverse: result block `blk`, lane group gq, pair p (result elements 2p, 2p + 1 = digits 0, 1)
+// hold sub-block 4 * sig_hi + sig_q and token tok_of.
+template <int MP>
+__host__ __device__ constexpr bool sig_hi(int blk, int p) {
+  return MP == 1 ? p == 1 : MP == 2 ? blk == 1 : blk >= 2;
+}
+template <int MP>
+__host__ __device__ constexpr int sig_q(int blk, int gq) {
+  return MP == 4 ? 2 * (blk & 1) + (gq >> 1) : gq;
+}
+template <int MP>
+__host__ __device__ constexpr int tok_of(int gq, int p) {
+  return MP == 1 ? 0 : MP == 2 ? p : 2 * (gq & 1) + p;
+}
+// Index of the {e, S} pair of (sub-block, token); the two pairs a lane reads for one result
+// block are adjacent, the first at an even index.
+template <int MP>
+__host__ __device__ constexpr int es_of(int sig, int t) {
+  return MP == 1 ? 2 * (sig & 3) + (sig >> 2) : sig * MP + t;
+}
+// Bytes of the operands of one super-block.
+template <int MP>
+__host__ __device__ constexpr size_t op_bytes() { return (size_t)MP * 1024 + (size_t)MP * 64; }
+
+// Byte k of each of a, b, c, d, packed into one word (a in byte 0).
+__device__ __forceinline__ uint32_t pack_byte(int a, int b, int c, int d, int k) {
+  const uint32_t lo = 0x0c0c0000u | (uint32_t)(4 + k) << 8 | (uint32_t)k;  // 0x0c selects 0
+  const uint32_t hi = (uint32_t)(4 + k) << 24 | (uint32_t)k << 16 | 0x0c0cu;
+  return __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, lo) |
+         __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, hi);
 }
 
-template <int M, bool LX>
-__global__ __launch_bounds__((LX && M == 1) ? 1024 : 512) void q4k_gemv_kernel(
+// Quantize one 32-value sub-block of one token (zeros when !valid) into the layout above.
+// A: operand entries of super-block slot bl; ES: its {e, S} pairs.
+template <int MP>
+__device__ __forceinline__ void quant_block(const float *__restrict__ x, bool valid, int sig,
+                                            int t, uint4 *__restrict__ A,
+                                            float2 *__restrict__ ES) {
+  float v[32];
+  if (valid) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 f = *reinterpret_cast<const float4 *>(x + 4 * i);
+      v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = 0.f;
+  }
+  float amax = 0.f, s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    amax = fmaxf(amax, fabsf(v[i]));
+    s += v[i];
+  }
+  // e = 2^k, the smallest power of two with 127 e >= amax (amax = f 2^E, f in [0.5, 1)), so
+  // x / e is exact and integer activations quantize without error. Non-finite blocks get
+  // e = NaN, which carries into every output that uses them.
+  int E;
+  const float f = frexpf(amax, &E);
+  const int k = E - 7 + (f > 127.f / 128.f ? 1 : 0);
+  float e = amax > 0.f ? ldexpf(1.f, k) : 0.f;
+  const float inv = amax > 0.f ? ldexpf(1.f, -k) : 0.f;
+  if (!(amax <= 3.4e38f)) e = __builtin_nanf("");
+  ES[es_of<MP>(sig, t)] = make_float2(e, s);
+
+  // T = rint(256 x / e), |T| <= 32512, so x ~= e T / 256 to within e / 512. The digits are
+  // q1 = (T + 128) >> 8 (byte 1 of T + 128) and q2 = T - 256 q1 in [-128, 127] (the low byte
+  // of T), as two's complement bytes: q1 + q2 / 256 = T / 256 exactly. Each lane group's eight
+  // values are written as soon as they are packed.
+  const float inv256 = inv * 256.f;
+  const int blk = blk_of<MP>(sig);
+  uint4 *row0 = A + ((size_t)blk * 16 + row_of<MP>(sig, t, 0)) * 4;
+  uint4 *row1 = A + ((size_t)blk * 16 + row_of<MP>(sig, t, 1)) * 4;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    int T[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) T[i] = __float2int_rn(v[8 * g + i] * inv256);
+    const uint32_t a0 = pack_byte(T[0] + 128, T[1] + 128, T[2] + 128, T[3] + 128, 1);
+    const uint32_t a1 = pack_byte(T[4] + 128, T[5] + 128, T[6] + 128, T[7] + 128, 1);
+    const uint32_t c0 = pack_byte(T[0], T[1], T[2], T[3], 0);
+    const uint32_t c1 = pack_byte(T[4], T[5], T[6], T[7], 0);
+    row0[g] = (sig & 1) ? make_uint4(0, 0, a0, a1) : make_uint4(a0, a1, 0, 0);
+    row1[g] = (sig & 1) ? make_uint4(0, 0, c0, c1) : make_uint4(c0, c1, 0, 0);
+  }
+}
+
+// Quantize super-blocks [s0, s0 + nb) of M tokens (tokens M..MP-1 zero) into slots 0..nb-1 of
+// the operand buffers, `lane` of `nlanes` threads sharing the work.
+template <int MP>
+__device__ __forceinline__ void quant_range(const float *__restrict__ X, int K, int M, int s0,
+                                            int nb, uint4 *__restrict__ A, float2 *__restrict__ ES,
+                                            int lane, int nlanes) {
+  const int per_t = nb * 8;
+  for (int task = lane; task < per_t * MP; task += nlanes) {
+    const int t = task / per_t, rest = task - t * per_t;
+    const int bl = rest >> 3, sig = rest & 7;
+    const bool valid = t < M;
+    quant_block<MP>(X + (valid ? (size_t)t * K + 256 * (size_t)(s0 + bl) + 32 * sig : 0), valid,
+                    sig, t, A + (size_t)bl * MP * 64, ES + (size_t)bl * 8 * MP);
+  }
+}
+
+// Scale and min of sub-block 4 * hi + q (GetScaleMinK4, internal/model/quantbits.go:42-47) from
+// the header words y = scales[0..3], z = scales[4..7], w = scales[8..11]; q may vary by lane.
+__device__ __forceinline__ void scale_min(uint32_t y, uint32_t z, uint32_t w, bool hi, int q,
+                                          float &sc, float &mn) {
+  const uint32_t o = 8u * (uint32_t)q;
+  uint32_t s, m;
+  if (!hi) {
+    s = __builtin_amdgcn_ubfe(y, o, 6);
+    m = __builtin_amdgcn_ubfe(z, o, 6);
+  } else {
+    s = __builtin_amdgcn_ubfe(w, o, 4) | (__builtin_amdgcn_ubfe(y, o + 6, 2) << 4);
+    m = __builtin_amdgcn_ubfe(w, o + 4, 4) | (__builtin_amdgcn_ubfe(z, o + 6, 2) << 4);
+  }
+  sc = (float)s;
+  mn = (float)m;
+}
+
+template <int MP, bool LX>
+__global__ __launch_bounds__(MP == 1 ? 1024 : 512) void q4k_gemv_i8_kernel(
     const uint8_t *__restrict__ W, const float *__restrict__ X, const uint4 *__restrict__ xg,
-    float *__restrict__ Y, int N, int K, int nblk, int ntiles, int TW, int KW) {
-  constexpr int R2 = 2 * M;             // operand rows (hi, lo per token)
-  constexpr int NSET = (R2 + 15) / 16;  // MFMA row sets
-  constexpr int J = M < 2 ? M : 2;      // tokens per lane group per set
+    float *__restrict__ Y, int N, int K, int M, int nblk, int ntiles, int TW, int KW) {
+  constexpr int NT = MP == 1 ? 1 : 2;  // token slots per lane
   extern __shared__ __align__(16) unsigned char smem[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, r = lane & 15;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: SGPRs
+  const int gq = lane >> 4, r = lane & 15;
   const int tile = wave / KW, part = wave - tile * KW;
   const int T = blockIdx.x * TW + tile;
   const bool tvalid = T < ntiles;
   const int b0 = (int)((long long)part * nblk / KW);
   const int b1 = (int)((long long)(part + 1) * nblk / KW);
-  const int ns = 8 * nblk;
+  const int nb = b1 - b0;  // super-blocks of this wave's K part (>= 1: KW <= nblk)
   const uint8_t *base = W + (size_t)(tvalid ? T : 0) * nblk * kQ4kRecord;
 
-  // Activation operands. LDS path: every wave stages its own K part into a private region
-  // (slices 8*b0 .. 8*b1 of size `cap` super-blocks), so no workgroup barrier precedes the
-  // first MFMA. Global path: one shared buffer for all of K.
-  const int cap = (nblk + KW - 1) / KW;  // super-blocks per part, rounded up
-  const uint4 *A;
-  const float *Sx;
-  int sbase;  // super-block index of A/Sx slice 0
-  if (LX) {
-    unsigned char *mine = smem + (size_t)wave * xop_bytes(M, 8 * cap);
-    A = reinterpret_cast<const uint4 *>(mine);
-    Sx = reinterpret_cast<const float *>(mine + xop_a_bytes(M, 8 * cap));
-    sbase = b0;
-  } else {
-    A = xg;
-    Sx = reinterpret_cast<const float *>(reinterpret_cast<const unsigned char *>(xg) +
-                                         xop_a_bytes(M, ns));
-    sbase = 0;
-  }
-  float *red = reinterpret_cast<float *>(smem + (LX ? (size_t)TW * KW * xop_bytes(M, 8 * cap) : 0));
+  // Operands for all of K (slot = super-block index): in LDS, quantized once by the whole
+  // workgroup for its TW tiles, or the prepared global buffer.
+  const unsigned char *opb = LX ? smem : reinterpret_cast<const unsigned char *>(xg);
+  const uint4 *A = reinterpret_cast<const uint4 *>(opb);
+  const float2 *ES = reinterpret_cast<const float2 *>(opb + (size_t)nblk * MP * 1024);
+  float *red = reinterpret_cast<float *>(smem + (LX ? (size_t)nblk * op_bytes<MP>() : 0));
 
-  // Operands of one super-block: the weight record and (global path) the activation operands.
+  // A lane's operand row belongs to one chunk per result block; with one or two tokens the
+  // lane loads only for the MFMA of that chunk.
+  auto lane_chunk = [&](int blk) {
+    const int p = (r >> 1) & 1;
+    const int sig = 4 * (sig_hi<MP>(blk, p) ? 1 : 0) + sig_q<MP>(blk, r >> 2);
+    return sig >> 1;
+  };
+  auto a_index = [&](int slot, int m) {  // this lane's entry for the MFMA of chunk m
+    const int blk = m * MP / 4;
+    return ((size_t)(slot * MP + blk) * 16 + r) * 4 + gq;
+  };
+  auto es_index = [&](int slot, int blk) {  // float4 holding this lane's two {e, S} pairs
+    return ((size_t)slot * 8 * MP +
+            es_of<MP>(4 * (sig_hi<MP>(blk, 0) ? 1 : 0) + sig_q<MP>(blk, gq), tok_of<MP>(gq, 0))) /
+           2;
+  };
+
   struct Ops {
     uint4 h, qa, qb;
-    f16x8 a[LX ? 1 : 8][NSET];
-    float s[LX ? 1 : NSET][J][8];
+    i32x4 a[LX ? 1 : 4];
+    float4 es[LX ? 1 : MP];
   };
   auto load = [&](int b, Ops &o) {
     const uint8_t *rec = base + (size_t)b * kQ4kRecord;
@@ -86,48 +226,41 @@ __global__ __launch_bounds__((LX && M == 1) ? 1024 : 512) void q4k_gemv_kernel(
     o.qb = *reinterpret_cast<const uint4 *>(rec + kQ4kHdr + 1024 + 16 * lane);
     if (!LX) {
 #pragma unroll
-      for (int s = 0; s < 8; ++s)
+      for (int m = 0; m < 4; ++m)
+        if (MP == 4 || lane_chunk(m * MP / 4) == m)
+          o.a[m] = __builtin_bit_cast(i32x4, A[a_index(b, m)]);
 #pragma unroll
-        for (int k = 0; k < NSET; ++k) {
-          const int rho = r + 16 * k, rr = rho < R2 ? rho : rho % R2;
-          o.a[s][k] = __builtin_bit_cast(f16x8, A[((8 * (b - sbase) + s) * 4 + g) * R2 + rr]);
-        }
-#pragma unroll
-      for (int k = 0; k < NSET; ++k)
-#pragma unroll
-        for (int jj = 0; jj < J; ++jj) {
-          const int t = 8 * k + 2 * g + jj, tt = t < M ? t : 0;
-          const float4 s0 = *reinterpret_cast<const float4 *>(Sx + ((b - sbase) * M + tt) * 8);
-          const float4 s1 = *reinterpret_cast<const float4 *>(Sx + ((b - sbase) * M + tt) * 8 + 4);
-          o.s[k][jj][0] = s0.x; o.s[k][jj][1] = s0.y; o.s[k][jj][2] = s0.z; o.s[k][jj][3] = s0.w;
-          o.s[k][jj][4] = s1.x; o.s[k][jj][5] = s1.y; o.s[k][jj][6] = s1.z; o.s[k][jj][7] = s1.w;
-        }
+      for (int blk = 0; blk < MP; ++blk)
+        o.es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b, blk)];
     }
   };
 
-  // PF records per wave in flight: a ring of register sets; a set is refilled with the record
-  // PF ahead as soon as its own record has been consumed.
-  constexpr int PF = LX ? 4 : (NSET == 1 ? 2 : 1);
+  constexpr int PF = LX ? 4 : 2;
   Ops ring[PF];
 #pragma unroll
-  for (int u = 0; u < PF; ++u)
-    if (b0 + u < b1) load(b0 + u, ring[u]);
-  if (LX) {
-    stage_x<M>(X, K, 8 * b0, 8 * (b1 - b0), ns, const_cast<uint4 *>(A), const_cast<float *>(Sx),
-               lane, 64);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (int u = 0; u < PF; ++u) {
+    if (!LX)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) ring[u].a[m] = i32x4{0, 0, 0, 0};
+    if (u < nb) load(b0 + u, ring[u]);
   }
-  const uint32_t kLoMask = in_reg(0x000F000Fu), kHiMask = in_reg(0x00F000F0u);
-  const uint32_t kMagic = in_reg(0x64006400u), k3F = in_reg(0x3F3F3F3Fu);
-  const uint32_t k0F = in_reg(0x0F0F0F0Fu), k30 = in_reg(0x30303030u);
+  // With the first records in flight, the workgroup quantizes the activations of all of K.
+  if (LX) {
+    quant_range<MP>(X, K, M, 0, nblk, const_cast<uint4 *>(A), const_cast<float2 *>(ES),
+                    threadIdx.x, blockDim.x);
+    __syncthreads();
+  }
+  const uint32_t k0F = 0x0F0F0F0Fu;
 
-  float acc[NSET][J];
+  // LDS path: the activation operands of the current super-block. Lanes that a given MFMA does
+  // not load for keep zeros there for the whole kernel.
+  i32x4 areg[4];
 #pragma unroll
-  for (int k = 0; k < NSET; ++k)
+  for (int m = 0; m < 4; ++m) areg[m] = i32x4{0, 0, 0, 0};
+
+  float acc[NT];
 #pragma unroll
-    for (int jj = 0; jj < J; ++jj) acc[k][jj] = 0.f;
+  for (int s = 0; s < NT; ++s) acc[s] = 0.f;
 
   for (int bb = b0; bb < b1; bb += PF) {
 #pragma unroll
@@ -136,219 +269,188 @@ __global__ __launch_bounds__((LX && M == 1) ? 1024 : 512) void q4k_gemv_kernel(
       if (b >= b1) break;
       Ops &cur = ring[u];
 
-      // Per-token sub-block sums of this super-block (rows of tokens >= M are never stored,
-      // so their lanes may use any finite value).
-      float S[NSET][J][8];
-#pragma unroll
-      for (int k = 0; k < NSET; ++k)
-#pragma unroll
-        for (int jj = 0; jj < J; ++jj) {
-          if (LX) {
-            const int t = 8 * k + 2 * g + jj, tt = t < M ? t : 0;
-            const float4 s0 = *reinterpret_cast<const float4 *>(Sx + ((b - sbase) * M + tt) * 8);
-            const float4 s1 = *reinterpret_cast<const float4 *>(Sx + ((b - sbase) * M + tt) * 8 + 4);
-            S[k][jj][0] = s0.x; S[k][jj][1] = s0.y; S[k][jj][2] = s0.z; S[k][jj][3] = s0.w;
-            S[k][jj][4] = s1.x; S[k][jj][5] = s1.y; S[k][jj][6] = s1.z; S[k][jj][7] = s1.w;
-          } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) S[k][jj][i] = cur.s[k][jj][i];
-          }
-        }
-
-      // d, dmin and the 8 six-bit (scale, min) pairs (GetScaleMinK4 geometry, byte-parallel):
-      // four packed bytes per word, then one v_cvt_f32_ubyteN per value.
-      const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(cur.h.x & 0xffffu));
-      const float dm = (float)__builtin_bit_cast(_Float16, (uint16_t)(cur.h.x >> 16));
-      const uint32_t scl = in_reg(cur.h.y & k3F), mnl = in_reg(cur.h.z & k3F);
-      const uint32_t sch = in_reg((cur.h.w & k0F) | ((cur.h.y >> 2) & k30));
-      const uint32_t mnh = in_reg(((cur.h.w >> 4) & k0F) | ((cur.h.z >> 2) & k30));
-      const uint32_t q[8] = {cur.qa.x, cur.qa.y, cur.qa.z, cur.qa.w,
-                             cur.qb.x, cur.qb.y, cur.qb.z, cur.qb.w};
-      const uint32_t scw[2] = {scl, sch}, mnw[2] = {mnl, mnh};
-      // Operand rows >= 2M only feed output rows that are never stored, so every lane loads a
-      // valid (finite) row instead of masking: no exec-mask juggling, no zero fills.
-      f16x8 aop[8][NSET];
+      float4 es[MP];
       if (LX) {
 #pragma unroll
-        for (int sidx = 0; sidx < 8; ++sidx)
+        for (int m = 0; m < 4; ++m)
+          if (MP == 4 || lane_chunk(m * MP / 4) == m)
+            areg[m] = __builtin_bit_cast(i32x4, A[a_index(b, m)]);
 #pragma unroll
-          for (int k = 0; k < NSET; ++k) {
-            const int rho = r + 16 * k, rr = rho < R2 ? rho : rho % R2;
-            aop[sidx][k] = __builtin_bit_cast(f16x8, A[((8 * (b - sbase) + sidx) * 4 + g) * R2 + rr]);
-          }
+        for (int blk = 0; blk < MP; ++blk)
+          es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b, blk)];
+      } else {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) areg[m] = cur.a[m];
+#pragma unroll
+        for (int blk = 0; blk < MP; ++blk) es[blk] = cur.es[blk];
       }
 
-      float aL[NSET][J], aH[NSET][J], V[NSET][J];
+      // Weight operands: chunk c = words 2c, 2c+1 of the lane's 32 bytes (8 nibble positions
+      // of the chunk), low nibbles -> slots 0-7 (sub-block 2c), high -> slots 8-15 (2c + 1).
+      const uint32_t q[8] = {cur.qa.x, cur.qa.y, cur.qa.z, cur.qa.w,
+                             cur.qb.x, cur.qb.y, cur.qb.z, cur.qb.w};
+      i32x4 D[MP];
 #pragma unroll
-      for (int k = 0; k < NSET; ++k)
-#pragma unroll
-        for (int jj = 0; jj < J; ++jj) aL[k][jj] = aH[k][jj] = V[k][jj] = 0.f;
-
-      // Phase 1: all 8 MFMAs of the record back to back (independent), so their latency
-      // overlaps; phase 2 scales and accumulates the results on the VALU.
-      f32x4 dres[4][2][NSET];
+      for (int blk = 0; blk < MP; ++blk) D[blk] = i32x4{0, 0, 0, 0};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const uint32_t x0 = q[2 * c], x1 = q[2 * c + 1];
-        const uint32_t y0 = x0 >> 8, y1 = x1 >> 8;
-        const f16x8 bl8 = __builtin_bit_cast(
-            f16x8, u32x4{(x0 & kLoMask) | kMagic, (y0 & kLoMask) | kMagic,
-                         (x1 & kLoMask) | kMagic, (y1 & kLoMask) | kMagic});
-        const f16x8 bh8 = __builtin_bit_cast(
-            f16x8, u32x4{(x0 & kHiMask) | kMagic, (y0 & kHiMask) | kMagic,
-                         (x1 & kHiMask) | kMagic, (y1 & kHiMask) | kMagic});
-#pragma unroll
-        for (int k = 0; k < NSET; ++k) {
-          const f16x8 al = LX ? aop[2 * c][k] : cur.a[2 * c][k];
-          const f16x8 ah = LX ? aop[2 * c + 1][k] : cur.a[2 * c + 1][k];
-          const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-          dres[c][0][k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bl8, z, 0, 0, 0);
-          dres[c][1][k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh8, z, 0, 0, 0);
-        }
+        const i32x4 B = {(int)(q[2 * c] & k0F), (int)(q[2 * c + 1] & k0F),
+                         (int)((q[2 * c] >> 4) & k0F), (int)((q[2 * c + 1] >> 4) & k0F)};
+        const int blk = c * MP / 4;
+        D[blk] = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[c], B, D[blk], 0, 0, 0);
       }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int sl = 2 * c, sh = 2 * c + 1;  // sub-blocks of the low / high nibbles of chunk c
-        const int bsel = (c & 1) * 2;  // byte of the packed word holding sc[sl]; sc[sh] is next
-        const uint32_t sw = scw[c >> 1], mw = mnw[c >> 1];
-        const float scL = (float)((sw >> (8 * bsel)) & 0xffu);
-        const float scH = (float)((sw >> (8 * bsel + 8)) & 0xffu);
-        const float mL = (float)((mw >> (8 * bsel)) & 0xffu);
-        const float mH = (float)((mw >> (8 * bsel + 8)) & 0xffu);
-#pragma unroll
-        for (int k = 0; k < NSET; ++k) {
-          const f32x4 dl = dres[c][0][k], dh = dres[c][1][k];
-#pragma unroll
-          for (int jj = 0; jj < J; ++jj) {
-            const float Sl = S[k][jj][sl], Sh = S[k][jj][sh];
-            const float tl = dl[2 * jj] + dl[2 * jj + 1];
-            const float th = dh[2 * jj] + dh[2 * jj + 1];
-            aL[k][jj] = fmaf(scL, fmaf(-1024.f, Sl, tl), aL[k][jj]);
-            aH[k][jj] = fmaf(scH, fmaf(-1024.f, Sh, th), aH[k][jj]);
-            V[k][jj] = fmaf(mL, Sl, fmaf(mH, Sh, V[k][jj]));
-          }
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < NSET; ++k)
-#pragma unroll
-        for (int jj = 0; jj < J; ++jj)
-          acc[k][jj] =
-              fmaf(d, fmaf(0.0625f, aH[k][jj], aL[k][jj]), fmaf(-dm, V[k][jj], acc[k][jj]));
+      // The slot is refilled with the record PF ahead as soon as its operands are consumed;
+      // the header words are kept for the scaling below.
+      const uint4 h = cur.h;
       if (b + PF < b1) load(b + PF, cur);
+
+      const float dd = (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xffffu));
+      const float dmn = (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16));
+      float xs[NT], vs[NT];
+#pragma unroll
+      for (int s = 0; s < NT; ++s) xs[s] = vs[s] = 0.f;
+#pragma unroll
+      for (int blk = 0; blk < MP; ++blk)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          float sc, mn;
+          scale_min(h.y, h.z, h.w, sig_hi<MP>(blk, p), sig_q<MP>(blk, gq), sc, mn);
+          const float val = fmaf((float)D[blk][2 * p + 1], 1.f / 256.f, (float)D[blk][2 * p]);
+          const float e = p ? es[blk].z : es[blk].x;
+          const float S = p ? es[blk].w : es[blk].y;
+          const int s = MP == 1 ? 0 : p;
+          xs[s] = fmaf(sc, e * val, xs[s]);
+          vs[s] = fmaf(mn, S, vs[s]);
+        }
+#pragma unroll
+      for (int s = 0; s < NT; ++s) acc[s] = fmaf(dd, xs[s], fmaf(-dmn, vs[s], acc[s]));
     }
   }
 
-  float vals[NSET * J];
+  // Partials of the KW parts go through LDS; part 0 sums them in part order (deterministic),
+  // then adds the lane groups that hold the same (token, row): all four (one or two tokens)
+  // or g and g ^ 2 (four tokens).
 #pragma unroll
-  for (int k = 0; k < NSET; ++k)
-#pragma unroll
-    for (int jj = 0; jj < J; ++jj) vals[k * J + jj] = acc[k][jj];
-  wg_reduce<NSET * J>(red, tile, part, KW, lane, vals);
+  for (int s = 0; s < NT; ++s) red[((tile * KW + part) * NT + s) * 64 + lane] = acc[s];
+  __syncthreads();
   const int row = T * 16 + r;
-  if (part != 0 || !tvalid || row >= N) return;
+  if (part != 0 || !tvalid) return;
+  float v[NT];
 #pragma unroll
-  for (int k = 0; k < NSET; ++k)
+  for (int s = 0; s < NT; ++s) {
+    v[s] = acc[s];
+    for (int q = 1; q < KW; ++q) v[s] += red[((tile * KW + q) * NT + s) * 64 + lane];
+    v[s] += __shfl_xor(v[s], 32);
+    if (MP <= 2) v[s] += __shfl_xor(v[s], 16);
+  }
+  if (row < N && gq < (MP == 4 ? 2 : 1)) {
 #pragma unroll
-    for (int jj = 0; jj < J; ++jj) {
-      const int t = 8 * k + 2 * g + jj;
-      if (t < M) Y[(size_t)t * N + row] = vals[k * J + jj];
+    for (int s = 0; s < NT; ++s) {
+      const int t = tok_of<MP>(gq, s);
+      if (t < M) Y[(size_t)t * N + row] = v[s];
     }
+  }
 }
 
-// One thread per (slice, token) into the global operand buffer; slices >= nsv are zero.
-template <int M>
-__global__ void gemv_xprep_kernel(const float *__restrict__ X, int K, int ns, int nsv,
-                                  uint4 *__restrict__ A) {
+// Global-path operand writer: one thread per (token, 32-value sub-block) of all of K.
+template <int MP>
+__global__ void gemv_i8_prep_kernel(const float *__restrict__ X, int K, int M, int nblk,
+                                    uint4 *__restrict__ A) {
   const int id = blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= ns * M) return;
-  const int t = id / ns, sl = id - t * ns;
-  float *S = reinterpret_cast<float *>(reinterpret_cast<unsigned char *>(A) + xop_a_bytes(M, ns));
-  split_slice<M>(X + (size_t)t * K + 32 * (sl < nsv ? sl : 0), sl < nsv, sl, t, A, S);
+  if (id >= MP * nblk * 8) return;
+  const int per_t = nblk * 8;
+  const int t = id / per_t, rest = id - t * per_t;
+  const int b = rest >> 3, sig = rest & 7;
+  float2 *ES = reinterpret_cast<float2 *>(reinterpret_cast<unsigned char *>(A) +
+                                          (size_t)nblk * MP * 1024);
+  const bool valid = t < M;
+  quant_block<MP>(X + (valid ? (size_t)t * K + 256 * (size_t)b + 32 * sig : 0), valid, sig, t,
+                  A + (size_t)b * MP * 64, ES + (size_t)b * 8 * MP);
 }
 
-template <int M>
-int launch_xprep_m(const float *X, int K, int ns, void *xop) {
-  const int n = ns * M, bs = 128;
-  gemv_xprep_kernel<M><<<ceil_div(n, bs), bs, 0, stream()>>>(X, K, ns, K / 32, (uint4 *)xop);
-  FHIP_CHECK_LAUNCH("gemv_xprep_kernel");
-  return FHIP_OK;
-}
-
-// Pick the workgroup shape: TW tiles x KW waves per tile (<= 16 waves per workgroup), aiming at
-// >= ~12 waves per CU in total. FAK_HIP_GEMV_TW / FAK_HIP_GEMV_KW override (tuning).
-void gemv_shape(int ntiles, int nblk, int max_waves, int &TW, int &KW) {
+// Workgroup shape: TW tiles x KW waves per tile (TW * KW <= max_waves). Measured on the 7B
+// and 27B FFN and lm_head shapes: each wave should stream >= ~6 records (KW), a workgroup
+// should be as wide as possible so its quantized activations serve many tiles (TW) while the
+// grid still covers about half the CUs, the grid should fit in one resident round when LDS
+// limits residency (large K), and very tall matrices prefer narrow workgroups.
+// FAK_HIP_GEMV_TW and FAK_HIP_GEMV_KW override (tuning).
+void i8_shape(int ntiles, int nblk, int max_waves, size_t lds_fixed, size_t lds_per_wave,
+              int &TW, int &KW) {
   const int cus = cu_count() > 0 ? cu_count() : 256;
+  const size_t lds_max = (size_t)lds_limit();
   TW = env_int("FAK_HIP_GEMV_TW");
   KW = env_int("FAK_HIP_GEMV_KW");
   if (KW <= 0) {
-    const int want_waves = 6 * cus;  // measured best on the 7B FFN shapes (KW=2 up, KW=8 down)
     KW = 1;
-    while (2 * KW <= max_waves && ntiles * KW < want_waves && nblk / (2 * KW) >= 2) KW *= 2;
+    while (2 * KW <= max_waves && nblk >= 6 * 2 * KW) KW *= 2;
+    // Small matrices: split K further until the grid has about two waves per CU.
+    while (2 * KW <= max_waves && ntiles * KW < 2 * cus && nblk >= 2 * 2 * KW) KW *= 2;
   }
   if (KW > nblk) KW = nblk;
   if (KW > max_waves) KW = max_waves;
-  if (TW <= 0) TW = 1;  // each wave stages its own K part: more tiles per WG would repeat it
+  if (TW <= 0) {
+    TW = max_waves / KW;
+    if (ntiles > 8 * cus) {
+      TW = 4 / KW > 1 ? 4 / KW : 1;
+    } else {
+      while (TW > 1 && ceil_div(ntiles, TW) < cus / 2) TW /= 2;
+      auto rounds = [&](int tw, int kw) {
+        const size_t lds = lds_fixed + (size_t)tw * kw * lds_per_wave;
+        const int by_lds = lds > 0 ? (int)(lds_max / lds) : 32;
+        const int per_cu = by_lds < 32 / (tw * kw) ? by_lds : 32 / (tw * kw);
+        return per_cu > 0 ? ceil_div(ceil_div(ntiles, tw), per_cu * cus) : 1 << 30;
+      };
+      while (KW > 1 && 2 * TW * (KW / 2) <= max_waves && rounds(TW, KW) > 1 &&
+             rounds(2 * TW, KW / 2) < rounds(TW, KW)) {
+        KW /= 2;
+        TW *= 2;
+      }
+    }
+  }
   if (TW < 1) TW = 1;
-  while (TW * KW > max_waves) TW--;
+  while (TW > 1 && TW * KW > max_waves) TW--;
 }
 
-template <int M>
-int launch_gemv(const uint8_t *W, const float *X, float *Y, int N, int K) {
-  const int nblk = K / 256, ntiles = q4k_tiles(N), ns = K / 32;
-  constexpr int VALS = ((2 * M + 15) / 16) * (M < 2 ? M : 2);
-  const int max_waves = M == 1 ? 16 : 8;
+template <int MP>
+int launch_i8(const uint8_t *W, const float *X, float *Y, int N, int K, int M) {
+  constexpr int NT = MP == 1 ? 1 : 2;
+  const int nblk = K / 256, ntiles = q4k_tiles(N);
+  const int max_waves = MP == 1 ? 16 : 8;
+  const size_t ldsx = (size_t)nblk * op_bytes<MP>();
   int TW, KW;
-  gemv_shape(ntiles, nblk, max_waves, TW, KW);
-  const int cap = ceil_div(nblk, KW);
-  const size_t redB = KW > 1 ? (size_t)TW * KW * 64 * VALS * 4 : 0;
-  const size_t ldsx = (size_t)TW * KW * xop_bytes(M, 8 * cap);
+  i8_shape(ntiles, nblk, max_waves, ldsx, (size_t)64 * NT * 4, TW, KW);
+  const size_t redB = (size_t)TW * KW * 64 * NT * 4;
   const bool lds_x = !env_int("FAK_HIP_GEMV_GLOBALX") && ldsx + redB <= (size_t)lds_limit();
-  if (!lds_x) gemv_shape(ntiles, nblk, 8, TW, KW);
   const int grid = ceil_div(ntiles, TW), threads = 64 * TW * KW;
   if (lds_x) {
-    q4k_gemv_kernel<M, true><<<grid, threads, ldsx + redB, stream()>>>(W, X, nullptr, Y, N, K,
-                                                                       nblk, ntiles, TW, KW);
-    FHIP_CHECK_LAUNCH("q4k_gemv_kernel<lds>");
+    q4k_gemv_i8_kernel<MP, true><<<grid, threads, ldsx + redB, stream()>>>(
+        W, X, nullptr, Y, N, K, M, nblk, ntiles, TW, KW);
+    FHIP_CHECK_LAUNCH("q4k_gemv_i8_kernel<lds>");
     return FHIP_OK;
   }
-  const size_t redG = KW > 1 ? (size_t)TW * KW * 64 * VALS * 4 : 0;
-  void *xop = workspace(xop_bytes(M, ns));
+  void *xop = workspace((size_t)nblk * op_bytes<MP>());
   if (!xop) return FHIP_ENOMEM;
-  if (int rc = launch_xprep_m<M>(X, K, ns, xop)) return rc;
-  q4k_gemv_kernel<M, false><<<grid, threads, redG, stream()>>>(W, X, (const uint4 *)xop, Y, N, K,
-                                                               nblk, ntiles, TW, KW);
-  FHIP_CHECK_LAUNCH("q4k_gemv_kernel<global>");
+  const int nprep = MP * nblk * 8;
+  gemv_i8_prep_kernel<MP><<<ceil_div(nprep, 128), 128, 0, stream()>>>(X, K, M, nblk,
+                                                                      (uint4 *)xop);
+  FHIP_CHECK_LAUNCH("gemv_i8_prep_kernel");
+  q4k_gemv_i8_kernel<MP, false><<<grid, threads, redB, stream()>>>(
+      W, X, (const uint4 *)xop, Y, N, K, M, nblk, ntiles, TW, KW);
+  FHIP_CHECK_LAUNCH("q4k_gemv_i8_kernel<global>");
   return FHIP_OK;
 }
 
 }  // namespace
 
-int launch_gemv_xprep(const float *X, int M, int K, int ns, void *xop) {
-#define FHIP_XPREP_CASE(m) \
-  case m: return launch_xprep_m<m>(X, K, ns, xop);
-  switch (M) {
-    FHIP_XPREP_CASE(1) FHIP_XPREP_CASE(2) FHIP_XPREP_CASE(3) FHIP_XPREP_CASE(4)
-    FHIP_XPREP_CASE(5) FHIP_XPREP_CASE(6) FHIP_XPREP_CASE(7) FHIP_XPREP_CASE(8)
-    FHIP_XPREP_CASE(9) FHIP_XPREP_CASE(10) FHIP_XPREP_CASE(11) FHIP_XPREP_CASE(12)
-    FHIP_XPREP_CASE(13) FHIP_XPREP_CASE(14) FHIP_XPREP_CASE(15) FHIP_XPREP_CASE(16)
-  }
-#undef FHIP_XPREP_CASE
-  return fail(FHIP_EINVAL, "gemv_xprep: M=%d outside 1..16", M);
-}
-
+// Small-M entry: 1..4 tokens on the int8 kernel (FAK_HIP_GEMV_WIDE=1 forces the f16 one),
+// 5..16 on the f16 kernel of q4k_gemv_wide.hip.
 int q4k_gemv(const void *Wv, const float *X, float *Y, int N, int K, int M) {
   const uint8_t *W = (const uint8_t *)Wv;
-#define FHIP_GEMV_CASE(m) \
-  case m: return launch_gemv<m>(W, X, Y, N, K);
-  switch (M) {
-    FHIP_GEMV_CASE(1) FHIP_GEMV_CASE(2) FHIP_GEMV_CASE(3) FHIP_GEMV_CASE(4)
-    FHIP_GEMV_CASE(5) FHIP_GEMV_CASE(6) FHIP_GEMV_CASE(7) FHIP_GEMV_CASE(8)
-    FHIP_GEMV_CASE(9) FHIP_GEMV_CASE(10) FHIP_GEMV_CASE(11) FHIP_GEMV_CASE(12)
-    FHIP_GEMV_CASE(13) FHIP_GEMV_CASE(14) FHIP_GEMV_CASE(15) FHIP_GEMV_CASE(16)
-  }
-#undef FHIP_GEMV_CASE
-  return fail(FHIP_EINVAL, "q4k_gemv: M=%d outside 1..16", M);
+  if (M < 1 || M > 16) return fail(FHIP_EINVAL, "q4k_gemv: M=%d outside 1..16", M);
+  if (M > 4 || env_int("FAK_HIP_GEMV_WIDE")) return q4k_gemv_wide(Wv, X, Y, N, K, M);
+  if (M == 1) return launch_i8<1>(W, X, Y, N, K, M);
+  if (M == 2) return launch_i8<2>(W, X, Y, N, K, M);
+  return launch_i8<4>(W, X, Y, N, K, M);
 }
 
 }  // namespace fhip
