@@ -9,10 +9,13 @@ the same names, argument meaning and failure behaviour (a Go panic becomes a Pyt
 * ``Tensor`` carries Dtype, Layout, Shape, QuantSpec and an opaque buffer (compute.go:168-175).
 * ``RocmBackend.Upload`` copies raw GGUF Q4_K bytes (``NewQ4K``, internal/compute/quant_q4k.go:
   37-44) or raw GGUF Q8_0 blocks resident in the tiled layout, caching by host buffer with an
-  element-count guard (cuda.go:690-704, 803-822); F32 activations upload verbatim.
+  element-count guard (cuda.go:690-704, 803-822); F32 activations upload verbatim. HAL Q8 weights
+  (``NewQ8``: int8 codes + f32 block scales, cpuref.go:53-56) upload as two device buffers, and
+  ``Upload(f32 weight, Q8_0)`` narrows on the device with quantizeVecQ8 (cuda.go:714-750).
 * ``MatMul(w, x)`` is y = x @ W^T (w [out,in], x [in] -> y [out]) and ``BatchedMatMul(w, X, P)``
   is the [P,in] -> [P,out] prefill GEMM, dispatched on ``w.Dtype`` (cuda.go:956-1035), each with
-  the reference's shape post-condition.
+  the reference's shape post-condition. On a HAL Q8 weight they quantize the activation on the
+  device and are bit-identical to cpuBackend.MatMul / BatchedMatMul (fhip_q8_matmul_f32).
 * The backend class is Approx (harness-enforced, compute.go:212-217, 525).
 
 Only the quantized weight path lives here; RMSNorm/RoPE/attention and the f32/f16 GEMMs are
@@ -135,6 +138,20 @@ def NewQ4K(be, shape, raw) -> Tensor:
                   QuantSpec(Block=256, Axis=2, Bits=4, Symmetric=False), HostBuf(i8=raw), be)
 
 
+class GGUFBlocks(HostBuf):
+    """Host bytes holding raw GGUF blocks (not HAL int8 codes)."""
+
+
+def NewQ8(be, shape, codes, scale, block: int = 32) -> Tensor:
+    """A HAL Q8_0 weight: int8 codes [out*in] + f32 per-block scales [out*in/block]
+    (internal/compute/cpuref.go:53-56)."""
+    codes = np.ascontiguousarray(codes, np.int8).reshape(-1)
+    scale = np.ascontiguousarray(scale, np.float32).reshape(-1)
+    return Tensor(Dtype.Q8_0, Layout.RowMajor, list(shape),
+                  QuantSpec(Block=block, Axis=2, Bits=8, Symmetric=True, Scale=scale),
+                  HostBuf(i8=codes), be)
+
+
 def NewQ8_0GGUF(be, shape, raw) -> Tensor:
     """Raw GGUF Q8_0 blocks (f16 d + 32 int8) as a host Q8_0 tensor. The scale is recorded per
     block as f32 (the exact widening of the stored f16), so the tensor carries the same values as
@@ -145,7 +162,23 @@ def NewQ8_0GGUF(be, shape, raw) -> Tensor:
     scale = blk[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1)
     return Tensor(Dtype.Q8_0, Layout.RowMajor, list(shape),
                   QuantSpec(Block=32, Axis=2, Bits=8, Symmetric=True, Scale=scale),
-                  HostBuf(i8=raw), be)
+                  GGUFBlocks(i8=raw), be)
+
+
+class DevQ8Buf:
+    """A device HAL Q8 weight: codes and scales buffers from the fakhip pool."""
+
+    def __init__(self, codes: int, scales: int, block: int, host_key=None):
+        self.ptr = codes
+        self.scales = scales
+        self.block = block
+        self.host_key = host_key
+
+    def Ready(self) -> bool:
+        return True
+
+
+Q8_DEVICE_BLOCK = 32  # q8DeviceBlock, internal/compute/cuda.go:210
 
 
 class RocmBackend:
@@ -174,17 +207,78 @@ class RocmBackend:
             raise TypeError("compute: rocm Upload expects host data")
         if t.Dtype == Dtype.Q4_K:
             return self._upload_quant(t, "fhip_q4k_upload", 256, 144)
-        if t.Dtype == Dtype.Q8_0:
+        if t.Dtype == Dtype.Q8_0 and isinstance(t.buf, GGUFBlocks):
             return self._upload_quant(t, "fhip_q8_0_upload", 32, 34)
+        if t.Dtype == Dtype.Q8_0:
+            return self._upload_hal_q8(t)
         if t.Dtype != Dtype.F32:
-            raise TypeError(f"compute: rocm Upload supports F32 host data or raw Q4_K / Q8_0 "
-                            f"blocks (got {t.Dtype})")
+            raise TypeError(f"compute: rocm Upload supports F32 host data, raw Q4_K / Q8_0 "
+                            f"blocks or HAL Q8 codes (got {t.Dtype})")
+        if as_ == Dtype.Q8_0:
+            return self._narrow_q8(t)
         f = t.buf.f32
         n = f.size * 4
         ptr = fakhip.alloc_call("fhip_malloc", max(n, 4))
         if n:
             fakhip.call("fhip_h2d", ptr, f.ctypes.data, n)
         return Tensor(Dtype.F32, Layout.RowMajor, list(t.Shape), None, DevBuf(ptr, n), self)
+
+    def _upload_hal_q8(self, t: Tensor) -> Tensor:
+        """A host HAL Q8 weight (codes + f32 scales) made resident as-is."""
+        if len(t.Shape) != 2 or t.Quant is None or t.Quant.Scale is None:
+            raise ValueError("compute: rocm Upload(Q8_0) expects a 2-D NewQ8 weight")
+        out, in_ = t.Shape
+        block = t.Quant.Block
+        codes, scale = t.buf.i8, t.Quant.Scale
+        if block <= 0 or in_ % block or codes.size != out * in_ or scale.size != out * (in_ // block):
+            raise ValueError(f"compute: Q8_0 weight [{out},{in_}] block {block} has {codes.size} "
+                             f"codes / {scale.size} scales")
+        key = (codes.ctypes.data, int(t.Dtype))
+        cached = self._upload_cache.get(key)
+        if cached is not None and cached.Numel() == t.Numel():
+            return cached
+        cp = fakhip.alloc_call("fhip_malloc", max(codes.size, 4))
+        sp = fakhip.alloc_call("fhip_malloc", max(scale.size * 4, 4))
+        if codes.size:
+            fakhip.call("fhip_h2d", cp, codes.ctypes.data, codes.size)
+            fakhip.call("fhip_h2d", sp, scale.ctypes.data, scale.size * 4)
+        res = Tensor(Dtype.Q8_0, Layout.RowMajor, [out, in_], t.Quant, DevQ8Buf(cp, sp, block, key),
+                     self)
+        self._upload_cache[key] = res
+        return res
+
+    def _narrow_q8(self, t: Tensor) -> Tensor:
+        """Upload(f32 weight, Q8_0): quantizeVecQ8 per row with the device block (cuda.go:714-750),
+        run on the device."""
+        if len(t.Shape) != 2:
+            raise ValueError("compute: rocm Upload(_, Q8_0) expects a 2-D [out,in] weight")
+        out, in_ = t.Shape
+        blk = Q8_DEVICE_BLOCK
+        if in_ % blk:
+            raise ValueError(f"compute: Q8_0 reduction dim {in_} not a multiple of {blk}")
+        f = t.buf.f32
+        if f.size != out * in_:
+            raise ValueError(f"compute: f32 weight has {f.size} elements, want {out}x{in_}")
+        key = (f.ctypes.data, int(Dtype.Q8_0))
+        cached = self._upload_cache.get(key)
+        if cached is not None and cached.Numel() == t.Numel():
+            return cached
+        nblk = in_ // blk
+        cp = fakhip.alloc_call("fhip_malloc", max(out * in_, 4))
+        sp = fakhip.alloc_call("fhip_malloc", max(out * nblk * 4, 4))
+        if f.size:
+            tmp = fakhip.alloc_call("fhip_malloc", f.size * 4)
+            try:
+                fakhip.call("fhip_h2d", tmp, f.ctypes.data, f.size * 4)
+                fakhip.call("fhip_q8_quantize_f32", tmp, cp, sp, out, in_, blk)
+                fakhip.call("fhip_sync")
+            finally:
+                fakhip.load().fhip_free(tmp)
+        res = Tensor(Dtype.Q8_0, Layout.RowMajor, [out, in_],
+                     QuantSpec(Block=blk, Axis=2, Bits=8, Symmetric=True),
+                     DevQ8Buf(cp, sp, blk, key), self)
+        self._upload_cache[key] = res
+        return res
 
     def _upload_quant(self, t: Tensor, fn: str, block: int, block_bytes: int) -> Tensor:
         if len(t.Shape) != 2:
@@ -218,11 +312,14 @@ class RocmBackend:
         return out
 
     def Free(self, t: Tensor) -> None:
-        if isinstance(t.buf, DevBuf) and t.buf.ptr:
+        if isinstance(t.buf, (DevBuf, DevQ8Buf)) and t.buf.ptr:
             if t.buf.host_key is not None:
                 self._upload_cache.pop(t.buf.host_key, None)
             fakhip.load().fhip_free(t.buf.ptr)
             t.buf.ptr = 0
+            if isinstance(t.buf, DevQ8Buf) and t.buf.scales:
+                fakhip.load().fhip_free(t.buf.scales)
+                t.buf.scales = 0
 
     # ---- the quantized matmul family ----
     def _dev_out(self, shape) -> Tensor:
@@ -240,6 +337,9 @@ class RocmBackend:
         y = self._dev_out(shape)
         if w.Dtype == Dtype.Q4_K:
             fakhip.call("fhip_q4k_matmul_f32", w.buf.ptr, X.buf.ptr, y.buf.ptr, out, in_, P)
+        elif w.Dtype == Dtype.Q8_0 and isinstance(w.buf, DevQ8Buf):
+            fakhip.call("fhip_q8_matmul_f32", w.buf.ptr, w.buf.scales, X.buf.ptr, y.buf.ptr, out,
+                        in_, P, w.buf.block)
         elif w.Dtype == Dtype.Q8_0:
             fakhip.call("fhip_q8_0_matmul_f32", w.buf.ptr, X.buf.ptr, y.buf.ptr, out, in_, P)
         else:

@@ -18,8 +18,11 @@ __host__ __device__ constexpr int perm8(int j) { return (j & 4) | ((j & 1) << 1)
 
 // Large-M activation operands for the GEMM: X [M][K] f32 -> f16 tiles in MFMA A-operand order:
 //   xa[((mt * (K/32) + s) * 64 + l)] = 8 f16 values f16(x[16 mt + (l & 15)][32 s + 8 (l >> 4)
-//   + perm8(j)]), rows past M are zero. Bytes: roundup(M,16) * K * 2.
-inline size_t gemm_xa_bytes(int M, int K) { return (size_t)ceil_div(M, 16) * 16 * K * 2; }
+//   + perm8(j)]), rows past M are zero. The 16-token tile count is padded to a multiple of
+//   kGemmTilePad so every workgroup's token tiles exist. Bytes: gemm_mt(M) * 16 * K * 2.
+constexpr int kGemmTilePad = 8;
+inline int gemm_mt(int M) { return ceil_div(ceil_div(M, 16), kGemmTilePad) * kGemmTilePad; }
+inline size_t gemm_xa_bytes(int M, int K) { return (size_t)gemm_mt(M) * 16 * K * 2; }
 int launch_gemm_xprep(const float *X, int M, int K, void *xa);
 
 int q4k_gemv(const void *W, const float *X, float *Y, int N, int K, int M);

@@ -9,8 +9,8 @@
 //     exponent trick) with one packed fma per pair of weights;
 //   * activations go global -> registers -> LDS (double-buffered, one 64-wide K chunk per
 //     stage) and are shared by the 4 waves;
-//   * the next super-block's weight records and the next stage's activation tiles are in
-//     flight while the current stage's MFMAs run.
+//   * weight record parts are reloaded for the next super-block as soon as they are consumed,
+//     and the next stage's activation tiles are in flight while the current stage's MFMAs run.
 // The f16 weight and activation rounding bound the error at max|dY|/RMS(Y) ~ 2e-3 (< 1e-2).
 #include "kernels.hpp"
 
@@ -77,89 +77,101 @@ __device__ __forceinline__ void dequant_chunk(uint32_t x0, uint32_t x1, const Ro
   bh = __builtin_bit_cast(f16x8, hh);
 }
 
+// Workgroup = 4 waves over TM 16-token tiles x 16 row tiles; wave w owns row tiles 4w..4w+3
+// (its weights stay in its registers) and all four share the token tiles through LDS.
 template <int TM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void q4k_gemm_kernel(const uint8_t *__restrict__ W,
-                                                       const uint4 *__restrict__ xa,
-                                                       float *__restrict__ Y, int N, int M,
-                                                       int nblk, int ntiles, int MT, int MTG) {
-  constexpr int AU = TM * 2 * 64;  // uint4 operand units per stage (TM tiles x 2 slices x 64)
-  constexpr int APT = AU / 256;    // per thread
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TM <= 4 ? 2 : 1, TM <= 4 ? 2 : 1))) void
+q4k_gemm_kernel(const uint8_t *__restrict__ W, const uint4 *__restrict__ xa,
+                float *__restrict__ Y, int N, int M, int nblk, int ntiles, int MTG, int remap) {
+  constexpr int R = 4;              // row tiles per wave
+  constexpr int AU = TM * 2 * 64;   // uint4 operand units per stage (TM tiles x 2 slices x 64)
+  constexpr int APT = AU / 256;     // per thread
   __shared__ uint4 As[2][AU];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int mtile = blockIdx.x % MTG, ntile = blockIdx.x / MTG;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2). The remap
+  // gives consecutive logical ids -- the token groups of one row group, which read the same
+  // weights -- to one XCD, so its L2 serves the repeated weight reads.
+  int wg = blockIdx.x;
+  if (remap) wg = (wg & 7) * (gridDim.x >> 3) + (wg >> 3);
+  const int mg = wg % MTG, ng = wg / MTG;
   const int nslices = nblk * 8;
-  const int rt0 = ntile * 16 + wave * 4;
+  const int rt0 = ng * 16 + wave * R;
+  const uint4 *xg = xa + (size_t)mg * TM * nslices * 64;  // this group's token tiles (padded)
 
-  f32x4 acc[TM][4];
+  f32x4 acc[TM][R];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < R; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  bool rvalid[4];
-  const uint8_t *rbase[4];
+  const uint8_t *rbase[R];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    rvalid[j] = rt0 + j < ntiles;
-    rbase[j] = W + (size_t)(rvalid[j] ? rt0 + j : 0) * nblk * kQ4kRecord;
-  }
+  for (int j = 0; j < R; ++j)
+    rbase[j] = W + (size_t)(rt0 + j < ntiles ? rt0 + j : 0) * nblk * kQ4kRecord;
 
-  auto load_a = [&](int st, uint4 *regs) {
-    const int b = st >> 2, c = st & 3;
+  // Stage st = chunk (64 K) st: token tile i, slice sl -> As[.][(2 i + sl) * 64 + l].
+  auto load_a = [&](int st, uint4 (&regs)[APT]) {
 #pragma unroll
     for (int k = 0; k < APT; ++k) {
       const int u = tid + 256 * k;
       const int i = u >> 7, sl = (u >> 6) & 1, l = u & 63;
-      const int mt = mtile * TM + i;
-      regs[k] = mt < MT ? xa[((size_t)mt * nslices + 8 * b + 2 * c + sl) * 64 + l]
-                        : make_uint4(0, 0, 0, 0);
+      regs[k] = xg[((size_t)i * nslices + 2 * st + sl) * 64 + l];
     }
   };
-  auto load_w = [&](int b, uint4 (&h)[4], uint4 (&qa)[4], uint4 (&qb)[4]) {
+  // Weight records: the header of the next super-block is loaded as soon as this one's scales
+  // are decoded; each half of the nibbles (qa: chunks 0-1, qb: chunks 2-3) is reloaded for the
+  // next super-block as soon as its second chunk is consumed, two chunks ahead of its use.
+  auto load_h = [&](int b, uint4 (&h)[R]) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint8_t *rec = rbase[j] + (size_t)b * kQ4kRecord;
-      h[j] = *reinterpret_cast<const uint4 *>(rec + 16 * (lane & 15));
-      qa[j] = *reinterpret_cast<const uint4 *>(rec + kQ4kHdr + 16 * lane);
-      qb[j] = *reinterpret_cast<const uint4 *>(rec + kQ4kHdr + 1024 + 16 * lane);
-    }
+    for (int j = 0; j < R; ++j)
+      h[j] = *reinterpret_cast<const uint4 *>(rbase[j] + (size_t)b * kQ4kRecord + 16 * (lane & 15));
+  };
+  auto load_q = [&](int b, int part, uint4 (&q)[R]) {
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+      q[j] = *reinterpret_cast<const uint4 *>(rbase[j] + (size_t)b * kQ4kRecord + kQ4kHdr +
+                                              1024 * part + 16 * lane);
   };
 
   uint4 areg[APT];
-  uint4 h[4], qa[4], qb[4], hn[4], qan[4], qbn[4];
-  load_w(0, h, qa, qb);
+  uint4 h[R], qa[R], qb[R];
+  load_h(0, h);
+  load_q(0, 0, qa);
+  load_q(0, 1, qb);
   load_a(0, areg);
 #pragma unroll
   for (int k = 0; k < APT; ++k) As[0][tid + 256 * k] = areg[k];
   __syncthreads();
 
-  RowScales rs[4];
   const int nst = nblk * 4;
   for (int b = 0; b < nblk; ++b) {
+    RowScales rs[R];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) rs[j] = row_scales(h[j]);
-    if (b + 1 < nblk) load_w(b + 1, hn, qan, qbn);
+    for (int j = 0; j < R; ++j) rs[j] = row_scales(h[j]);
+    const bool more = b + 1 < nblk;
+    if (more) load_h(b + 1, h);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int st = 4 * b + c, cur = c & 1;  // 4 stages per super-block: parity == c & 1
       if (st + 1 < nst) load_a(st + 1, areg);
-      f16x8 bl[4], bh[4];
+      f16x8 bl[R], bh[R];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < R; ++j) {
         const uint4 q = c < 2 ? qa[j] : qb[j];
         const uint32_t x0 = (c & 1) ? q.z : q.x, x1 = (c & 1) ? q.w : q.y;
         dequant_chunk(x0, x1, rs[j], c, bl[j], bh[j]);
       }
+      if (more && c == 1) load_q(b + 1, 0, qa);
+      if (more && c == 3) load_q(b + 1, 1, qb);
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        if (mtile * TM + i < MT) {
-          const f16x8 al = __builtin_bit_cast(f16x8, As[cur][(2 * i) * 64 + lane]);
-          const f16x8 ah = __builtin_bit_cast(f16x8, As[cur][(2 * i + 1) * 64 + lane]);
+        const f16x8 al = __builtin_bit_cast(f16x8, As[cur][(2 * i) * 64 + lane]);
+        const f16x8 ah = __builtin_bit_cast(f16x8, As[cur][(2 * i + 1) * 64 + lane]);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bl[j], acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[j], acc[i][j], 0, 0, 0);
-          }
+        for (int j = 0; j < R; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bl[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[j], acc[i][j], 0, 0, 0);
         }
       }
       if (st + 1 < nst) {
@@ -168,24 +180,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       }
       __syncthreads();
     }
-    if (b + 1 < nblk) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        h[j] = hn[j];
-        qa[j] = qan[j];
-        qb[j] = qbn[j];
-      }
-    }
   }
 
   const int g = lane >> 4, r = lane & 15;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    const int tbase = 16 * (mtile * TM + i) + 4 * g;
+    const int tbase = 16 * (mg * TM + i) + 4 * g;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < R; ++j) {
       const int o = 16 * (rt0 + j) + r;
-      if (!rvalid[j] || o >= N) continue;
+      if (rt0 + j >= ntiles || o >= N) continue;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t = tbase + e;
@@ -197,9 +201,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 
 template <int TM>
 int launch_gemm(const uint8_t *W, const uint4 *xa, float *Y, int N, int M, int nblk) {
-  const int ntiles = q4k_tiles(N), MT = ceil_div(M, 16), MTG = ceil_div(MT, TM);
+  const int ntiles = q4k_tiles(N), MTG = gemm_mt(M) / TM;
   const int NTG = ceil_div(ntiles, 16);
-  q4k_gemm_kernel<TM><<<MTG * NTG, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MT, MTG);
+  const int grid = MTG * NTG;
+  // XCD-grouped order is opt-in (FAK_HIP_GEMM_REMAP=1): measured 2-20% slower on the C3 shapes.
+  const int remap = (grid % 8 == 0 && env_int("FAK_HIP_GEMM_REMAP")) ? 1 : 0;
+  q4k_gemm_kernel<TM><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG, remap);
   FHIP_CHECK_LAUNCH("q4k_gemm_kernel");
   return FHIP_OK;
 }
@@ -213,13 +220,12 @@ int q4k_gemm(const void *Wv, const float *X, float *Y, int N, int K, int M) {
   if (!xa) return FHIP_ENOMEM;
   if (int rc = launch_gemm_xprep(X, M, K, xa)) return rc;
   int tm = env_int("FAK_HIP_GEMM_TM");
-  if (tm == 0) tm = M <= 64 ? 4 : (M <= 256 ? 8 : 16);
+  if (tm == 0) tm = 4;
   switch (tm) {
     case 4: return launch_gemm<4>(W, xa, Y, N, M, nblk);
     case 8: return launch_gemm<8>(W, xa, Y, N, M, nblk);
-    case 16: return launch_gemm<16>(W, xa, Y, N, M, nblk);
   }
-  return fail(FHIP_EINVAL, "q4k_gemm: FAK_HIP_GEMM_TM=%d not in {4,8,16}", tm);
+  return fail(FHIP_EINVAL, "q4k_gemm: FAK_HIP_GEMM_TM=%d not in {4,8}", tm);
 }
 
 }  // namespace fhip

@@ -44,7 +44,7 @@ int env_int(const char *name) {
 
 int launch_gemm_xprep(const float *X, int M, int K, void *xa) {
   const int nslices = K / 32;
-  const long long total = (long long)ceil_div(M, 16) * nslices * 64;
+  const long long total = (long long)gemm_mt(M) * nslices * 64;
   const int bs = 256;
   gemm_xprep_kernel<<<(unsigned)((total + bs - 1) / bs), bs, 0, stream()>>>(X, M, K, nslices,
                                                                            total, (uint4 *)xa);

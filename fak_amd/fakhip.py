@@ -66,6 +66,8 @@ SIGNATURES = {
     "fhip_q8_0_dequant_f32": (_i, [_vp, _vp, _i, _i]),
     "fhip_q8_0_upload": (_vp, [_vp, _i, _i]),
     "fhip_q8_0_matmul_f32": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "fhip_q8_quantize_f32": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "fhip_q8_matmul_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i]),
 }
 
 _lib = None

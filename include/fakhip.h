@@ -119,6 +119,25 @@ void *fhip_q8_0_upload(const uint8_t *hRaw, int out, int in);
 int fhip_q8_0_matmul_f32(const void *dPacked, const float *dX, float *dY, int out, int in,
                          int P);
 
+/* ---- HAL Q8 lane: int8 codes [out][in] + f32 scales [out][in/block], activation quantized on
+ * the device (compute.NewQ8 tensors, internal/compute/cpuref.go:53-56) ------------------- */
+
+/* quantizeVecQ8 (internal/compute/cpuref.go:505-527) of each row of X[rows][in]:
+ * scales[r][b] = amax/127, codes = q8round(x / scale) (internal/model/quant.go:89-104),
+ * all-zero blocks give scale 0 and zero codes. Bit-identical to the CPU reference. The device
+ * form of Upload(F32, Q8_0) narrowing (internal/compute/cuda.go:714-750) and of the activation
+ * quantization k_q8_quant_act (internal/compute/cuda_kernels.cu:374-398). */
+int fhip_q8_quantize_f32(const float *dX, int8_t *dCodes, float *dScales, int rows, int in,
+                         int block);
+/* Y[P,out] = X[P,in] @ W^T on a HAL Q8 weight: the replacement for fcuda_q8_matmul_f32
+ * (internal/compute/cuda_backend.h:110-111), same arguments. X is quantized per row on the
+ * device (quantizeVecQ8), then P == 1 follows qdot8scalar (cpuref.go:532-548, MatMul) and
+ * P > 1 follows qgemm8cell with 16 lanes (cpuref.go:553-577, BatchedMatMul): results are
+ * bit-identical to cpuBackend.MatMul / BatchedMatMul. block must divide in and be a multiple of
+ * 4; P > 1 needs block >= 32 (the reference reads 16 pairs per block). dCodes 4-byte aligned. */
+int fhip_q8_matmul_f32(const int8_t *dCodes, const float *dScales, const float *dX, float *dY,
+                       int out, int in, int P, int block);
+
 #ifdef __cplusplus
 }
 #endif
