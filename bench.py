@@ -281,6 +281,7 @@ def bench_decode_stack(steps, warmup, ev, layers=28):
     head = Weight("q4k", V, H, 60, 1)
     xs = {k: Buf(k * 4, synth.activations(1, k, 70 + k)[0]) for k in (H, F)}
     ys = {n: Buf(n * 4) for n in (H, KV, F, V)}
+    ys_v = Buf(KV * 4)  # v's output (k uses ys[KV]) so a group's members never share an output
     calls = []
     for l in range(layers):
         for (n, k), p in zip(layer_shapes, per_layer[l]):
@@ -289,6 +290,29 @@ def bench_decode_stack(steps, warmup, ev, layers=28):
     calls.append(("fhip_q4k_matmul_f32",
                   lambda i: (head.ptrs[0], xs[H].ptr, ys[V].ptr, V, H, 1)))
     ms, per = time_calls(calls, steps, warmup, ev)
+    # The same token with a layer's q/k/v and gate/up each run as one group launch (the
+    # reference's q4kGroupDispatch, internal/model/metal_q4k_on.go:139-190): 4 launches per layer.
+    groups = []
+    gcalls = []
+    for l in range(layers):
+        p = per_layer[l]
+        for members in ((0, 1, 2), (4, 5)):
+            n = len(members)
+            wp = (C.c_void_p * n)(*[p[m] for m in members])
+            yp = (C.c_void_p * n)(*[ys[layer_shapes[m][0]].ptr if m != 2 else ys_v.ptr
+                                    for m in members])
+            op = (C.c_int * n)(*[layer_shapes[m][0] for m in members])
+            groups.append((wp, yp, op))
+            gcalls.append(("fhip_q4k_matmul_group_f32",
+                           lambda i, g=groups[-1], n=n: (C.addressof(g[0]), C.addressof(g[1]),
+                                                         C.addressof(g[2]), n, xs[H].ptr, H, 1)))
+            if members == (0, 1, 2):
+                gcalls.append(("fhip_q4k_matmul_f32",
+                               lambda i, p=p: (p[3], xs[H].ptr, ys[H].ptr, H, H, 1)))
+        gcalls.append(("fhip_q4k_matmul_f32", lambda i, p=p: (p[6], xs[F].ptr, ys[H].ptr, H, F, 1)))
+    gcalls.append(("fhip_q4k_matmul_f32",
+                   lambda i: (head.ptrs[0], xs[H].ptr, ys[V].ptr, V, H, 1)))
+    gms, _ = time_calls(gcalls, steps, warmup, ev)
     wbytes = layers * sum(q4k_bytes(n, k) for n, k in layer_shapes) + q4k_bytes(V, H)
     abytes = layers * sum(4 * (n + k) for n, k in layer_shapes) + 4 * (V + H)
     for l in range(1, layers):
@@ -296,13 +320,17 @@ def bench_decode_stack(steps, warmup, ev, layers=28):
             fakhip.load().fhip_free(p)
     for w in base + [head]:
         w.free()
-    for b in list(xs.values()) + list(ys.values()):
+    for b in list(xs.values()) + list(ys.values()) + [ys_v]:
         b.free()
     return {"layers": layers, "gemvs_per_token": len(calls), "weight_bytes": wbytes,
             "ms_per_token": ms, "tok_per_s": 1e3 / ms,
             "GBs": (wbytes + abytes) / (ms * 1e6),
             "pct_hbm_peak": 100.0 * (wbytes + abytes) / (ms * 1e6) / HBM_PEAK_GBS,
-            "sum_of_call_ms": sum(per)}
+            "sum_of_call_ms": sum(per),
+            "grouped_qkv_gateup": {"launches_per_token": len(gcalls), "ms_per_token": gms,
+                                   "tok_per_s": 1e3 / gms,
+                                   "pct_hbm_peak": 100.0 * (wbytes + abytes) / (gms * 1e6)
+                                   / HBM_PEAK_GBS}}
 
 
 def cpu_baseline(ws, xs, ys, budget_s=10.0):

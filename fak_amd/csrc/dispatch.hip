@@ -25,4 +25,39 @@ int fhip_q4k_matmul_f32(const void *dPacked, const float *dX, float *dY, int out
   return q4k_gemm(dPacked, dX, dY, out, in, P);
 }
 
+int fhip_q4k_matmul_group_f32(const void *const *dPacked, float *const *dY, const int *out,
+                              int count, const float *dX, int in, int P) {
+  clear_error();
+  if (count < 1 || count > kMaxGroup)
+    return fail(FHIP_EINVAL, "fhip_q4k_matmul_group_f32: count=%d outside 1..%d", count,
+                kMaxGroup);
+  if (!dPacked || !dY || !out || !dX)
+    return fail(FHIP_EINVAL, "fhip_q4k_matmul_group_f32: null pointer");
+  if (in <= 0 || in % 256 != 0)
+    return fail(FHIP_EINVAL, "fhip_q4k_matmul_group_f32: in=%d not a positive multiple of 256",
+                in);
+  if (P < 0) return fail(FHIP_EINVAL, "fhip_q4k_matmul_group_f32: P=%d < 0", P);
+  if ((uintptr_t)dX & 15)
+    return fail(FHIP_EINVAL, "fhip_q4k_matmul_group_f32: dX must be 16-byte aligned");
+  GemvGroup g = {};
+  g.count = count;
+  g.tile0[0] = 0;
+  for (int i = 0; i < count; ++i) {
+    if (!dPacked[i] || !dY[i] || out[i] <= 0 || ((uintptr_t)dPacked[i] & 15))
+      return fail(FHIP_EINVAL, "fhip_q4k_matmul_group_f32: member %d: null or misaligned "
+                               "pointer or out=%d", i, out[i]);
+    g.W[i] = (const uint8_t *)dPacked[i];
+    g.Y[i] = dY[i];
+    g.N[i] = out[i];
+    g.tile0[i + 1] = g.tile0[i] + q4k_tiles(out[i]);
+  }
+  if (P == 0) return FHIP_OK;
+  int gemv_max = env_int("FAK_HIP_GEMV_MAX_M");
+  if (gemv_max <= 0 || gemv_max > 16) gemv_max = 16;
+  if (P <= gemv_max) return q4k_gemv_group(g, dX, in, P);
+  for (int i = 0; i < count; ++i)
+    if (int rc = q4k_gemm(dPacked[i], dX, dY[i], out[i], in, P)) return rc;
+  return FHIP_OK;
+}
+
 }  // extern "C"

@@ -26,6 +26,17 @@ inline size_t gemm_xa_bytes(int M, int K) { return (size_t)gemm_mt(M) * 16 * K *
 int launch_gemm_xprep(const float *X, int M, int K, void *xa);
 
 int q4k_gemv(const void *W, const float *X, float *Y, int N, int K, int M);
+// Matrices sharing one activation, run as one grid (the group dispatch of
+// internal/model/metal_q4k_on.go:139-190). Members are concatenated by 16-row tiles.
+constexpr int kMaxGroup = 8;
+struct GemvGroup {
+  const uint8_t *W[kMaxGroup];
+  float *Y[kMaxGroup];
+  int N[kMaxGroup];
+  int tile0[kMaxGroup + 1];  // first tile of each member; tile0[count] = total tiles
+  int count;
+};
+int q4k_gemv_group(const GemvGroup &g, const float *X, int K, int M);
 int q4k_gemv_wide(const void *W, const float *X, float *Y, int N, int K, int M);
 int q4k_gemm(const void *W, const float *X, float *Y, int N, int K, int M);
 int q8_0_gemv(const void *W, const float *X, float *Y, int N, int K, int M);

@@ -175,20 +175,26 @@ __device__ __forceinline__ void scale_min(uint32_t y, uint32_t z, uint32_t w, bo
 
 template <int MP, bool LX>
 __global__ __launch_bounds__(MP == 1 ? 1024 : 512) void q4k_gemv_i8_kernel(
-    const uint8_t *__restrict__ W, const float *__restrict__ X, const uint4 *__restrict__ xg,
-    float *__restrict__ Y, int N, int K, int M, int nblk, int ntiles, int TW, int KW) {
+    const GemvGroup grp, const float *__restrict__ X, const uint4 *__restrict__ xg, int K, int M,
+    int nblk, int TW, int KW) {
   constexpr int NT = MP == 1 ? 1 : 2;  // token slots per lane
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: SGPRs
   const int gq = lane >> 4, r = lane & 15;
   const int tile = wave / KW, part = wave - tile * KW;
-  const int T = blockIdx.x * TW + tile;
-  const bool tvalid = T < ntiles;
+  const int Tg = blockIdx.x * TW + tile;  // tile of the concatenated group
+  const int ntiles = grp.tile0[grp.count];
+  const bool tvalid = Tg < ntiles;
+  int mem = 0;  // the member this tile belongs to (wave-uniform scalar search)
+  while (mem + 1 < grp.count && Tg >= grp.tile0[mem + 1]) ++mem;
+  const int T = tvalid ? Tg - grp.tile0[mem] : 0;  // tile within the member
+  const int N = grp.N[mem];
+  float *__restrict__ Y = grp.Y[mem];
   const int b0 = (int)((long long)part * nblk / KW);
   const int b1 = (int)((long long)(part + 1) * nblk / KW);
   const int nb = b1 - b0;  // super-blocks of this wave's K part (>= 1: KW <= nblk)
-  const uint8_t *base = W + (size_t)(tvalid ? T : 0) * nblk * kQ4kRecord;
+  const uint8_t *base = grp.W[mem] + (size_t)T * nblk * kQ4kRecord;
 
   // Operands for all of K (slot = super-block index): in LDS, quantized once by the whole
   // workgroup for its TW tiles, or the prepared global buffer.
@@ -412,9 +418,9 @@ void i8_shape(int ntiles, int nblk, int max_waves, size_t lds_fixed, size_t lds_
 }
 
 template <int MP>
-int launch_i8(const uint8_t *W, const float *X, float *Y, int N, int K, int M) {
+int launch_i8(const GemvGroup &g, const float *X, int K, int M) {
   constexpr int NT = MP == 1 ? 1 : 2;
-  const int nblk = K / 256, ntiles = q4k_tiles(N);
+  const int nblk = K / 256, ntiles = g.tile0[g.count];
   const int max_waves = MP == 1 ? 16 : 8;
   const size_t ldsx = (size_t)nblk * op_bytes<MP>();
   int TW, KW;
@@ -423,8 +429,8 @@ int launch_i8(const uint8_t *W, const float *X, float *Y, int N, int K, int M) {
   const bool lds_x = !env_int("FAK_HIP_GEMV_GLOBALX") && ldsx + redB <= (size_t)lds_limit();
   const int grid = ceil_div(ntiles, TW), threads = 64 * TW * KW;
   if (lds_x) {
-    q4k_gemv_i8_kernel<MP, true><<<grid, threads, ldsx + redB, stream()>>>(
-        W, X, nullptr, Y, N, K, M, nblk, ntiles, TW, KW);
+    q4k_gemv_i8_kernel<MP, true><<<grid, threads, ldsx + redB, stream()>>>(g, X, nullptr, K, M,
+                                                                           nblk, TW, KW);
     FHIP_CHECK_LAUNCH("q4k_gemv_i8_kernel<lds>");
     return FHIP_OK;
   }
@@ -434,10 +440,16 @@ int launch_i8(const uint8_t *W, const float *X, float *Y, int N, int K, int M) {
   gemv_i8_prep_kernel<MP><<<ceil_div(nprep, 128), 128, 0, stream()>>>(X, K, M, nblk,
                                                                       (uint4 *)xop);
   FHIP_CHECK_LAUNCH("gemv_i8_prep_kernel");
-  q4k_gemv_i8_kernel<MP, false><<<grid, threads, redB, stream()>>>(
-      W, X, (const uint4 *)xop, Y, N, K, M, nblk, ntiles, TW, KW);
+  q4k_gemv_i8_kernel<MP, false><<<grid, threads, redB, stream()>>>(g, X, (const uint4 *)xop, K,
+                                                                   M, nblk, TW, KW);
   FHIP_CHECK_LAUNCH("q4k_gemv_i8_kernel<global>");
   return FHIP_OK;
+}
+
+int launch_i8_any(const GemvGroup &g, const float *X, int K, int M) {
+  if (M == 1) return launch_i8<1>(g, X, K, M);
+  if (M == 2) return launch_i8<2>(g, X, K, M);
+  return launch_i8<4>(g, X, K, M);
 }
 
 }  // namespace
@@ -445,12 +457,28 @@ int launch_i8(const uint8_t *W, const float *X, float *Y, int N, int K, int M) {
 // Small-M entry: 1..4 tokens on the int8 kernel (FAK_HIP_GEMV_WIDE=1 forces the f16 one),
 // 5..16 on the f16 kernel of q4k_gemv_wide.hip.
 int q4k_gemv(const void *Wv, const float *X, float *Y, int N, int K, int M) {
-  const uint8_t *W = (const uint8_t *)Wv;
   if (M < 1 || M > 16) return fail(FHIP_EINVAL, "q4k_gemv: M=%d outside 1..16", M);
   if (M > 4 || env_int("FAK_HIP_GEMV_WIDE")) return q4k_gemv_wide(Wv, X, Y, N, K, M);
-  if (M == 1) return launch_i8<1>(W, X, Y, N, K, M);
-  if (M == 2) return launch_i8<2>(W, X, Y, N, K, M);
-  return launch_i8<4>(W, X, Y, N, K, M);
+  GemvGroup g = {};
+  g.W[0] = (const uint8_t *)Wv;
+  g.Y[0] = Y;
+  g.N[0] = N;
+  g.tile0[0] = 0;
+  g.tile0[1] = q4k_tiles(N);
+  g.count = 1;
+  return launch_i8_any(g, X, K, M);
+}
+
+// A group (1..kMaxGroup members, one activation): one grid over all members' tiles for 1..4
+// tokens; wider batches run the members one after another.
+int q4k_gemv_group(const GemvGroup &g, const float *X, int K, int M) {
+  if (M < 1 || M > 16) return fail(FHIP_EINVAL, "q4k_gemv_group: M=%d outside 1..16", M);
+  if (M > 4 || env_int("FAK_HIP_GEMV_WIDE")) {
+    for (int i = 0; i < g.count; ++i)
+      if (int rc = q4k_gemv_wide(g.W[i], X, g.Y[i], g.N[i], K, M)) return rc;
+    return FHIP_OK;
+  }
+  return launch_i8_any(g, X, K, M);
 }
 
 }  // namespace fhip

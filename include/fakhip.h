@@ -104,6 +104,14 @@ void *fhip_q4k_upload(const uint8_t *hRaw, int out, int in);
  * Error bound vs the f32 reference: GEMV max|dY|/RMS(Y) <= 1e-3, GEMM <= 1e-2. */
 int fhip_q4k_matmul_f32(const void *dPacked, const float *dX, float *dY, int out, int in,
                         int P);
+/* count (1..8) tiled Q4_K weights [out[i]][in] that share one activation X[P,in] (a layer's
+ * q/k/v or gate/up): Y_i = X @ W_i^T for each i — the group dispatch of q4kGroupDispatch /
+ * metalgemm.GEMVGroup (internal/model/metal_q4k_on.go:139-190), which runs the members in one
+ * command buffer. dPacked, dY and out are host arrays of device pointers / row counts. For
+ * P <= 4 the members run as one grid that quantizes X once; otherwise one call per member.
+ * Each Y_i meets the fhip_q4k_matmul_f32 bound (not bit-identical to it: the K split may differ). */
+int fhip_q4k_matmul_group_f32(const void *const *dPacked, float *const *dY, const int *out,
+                              int count, const float *dX, int in, int P);
 
 /* ---- Q8_0 (32-weight blocks of 34 B: f16 d + 32 int8; internal/ggufload/gguf.go:24) ----- */
 

@@ -75,3 +75,27 @@ def q8_0_matmul(raw: np.ndarray, out: int, in_: int, X: np.ndarray, P: int) -> n
             return dy.to_host(np.float32).reshape(P, out)
     finally:
         lib.fhip_free(w)
+
+
+def q4k_matmul_group(raws, outs, in_: int, X: np.ndarray, P: int) -> list:
+    """Upload each raw Q4_K member, run fhip_q4k_matmul_group_f32 on the shared X[P, in],
+    return [Y_i[P, out_i]]."""
+    import ctypes as C
+    lib = fakhip.load()
+    ws = [fakhip.alloc_call("fhip_q4k_upload", np.ascontiguousarray(r).ctypes.data, o, in_)
+          for r, o in zip(raws, outs)]
+    ys = [Dev(P * o * 4) for o in outs]
+    try:
+        with Dev.from_host(np.ascontiguousarray(X, np.float32)) as dx:
+            n = len(outs)
+            wp = (C.c_void_p * n)(*ws)
+            yp = (C.c_void_p * n)(*[y.ptr for y in ys])
+            op = (C.c_int * n)(*outs)
+            fakhip.call("fhip_q4k_matmul_group_f32", C.addressof(wp), C.addressof(yp),
+                        C.addressof(op), n, dx.ptr, in_, P)
+            return [y.to_host(np.float32).reshape(P, o) for y, o in zip(ys, outs)]
+    finally:
+        for y in ys:
+            y.close()
+        for w in ws:
+            lib.fhip_free(w)

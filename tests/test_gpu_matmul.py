@@ -120,3 +120,36 @@ def test_q4k_integer_fixture_exact(hip, oracle_mod):
     x = np.array([(i * 13) % 29 - 14 for i in range(in_)], np.float32)
     Y = q4k_matmul(raw, out, in_, x[None], 1)[0]
     np.testing.assert_array_equal(Y, oracle_mod.q4k_matrows(raw, out, in_, x))
+
+
+@pytest.mark.parametrize("P", [1, 3, 4, 8, 40])
+def test_q4k_group_qkv(hip, oracle_mod, P):
+    """A layer's q/k/v sharing one activation (3584 -> 3584, 512, 512) through the group entry:
+    every member within the GEMV (P <= 16) or GEMM bound of its own oracle result, and within
+    the same bound of the single-matrix entry."""
+    from tests.gpu_util import q4k_matmul_group
+    in_, outs = 3584, [3584, 512, 512]
+    print(f"[case] q4k group qkv in={in_} outs={outs} P={P}", flush=True)
+    raws = [synth.q4k_weights(o, in_, seed=300 + i) for i, o in enumerate(outs)]
+    X = synth.activations(P, in_, seed=399)
+    Ys = q4k_matmul_group(raws, outs, in_, X, P)
+    tol = GEMV_TOL if P <= 16 else GEMM_TOL
+    for raw, o, Y in zip(raws, outs, Ys):
+        ref = oracle_mod.q4k_gemm(raw, o, in_, X, P, workers=16)
+        e = rel_err(Y, ref)
+        single = q4k_matmul(raw, o, in_, X, P)
+        print(f"    out={o}: max|d|/RMS = {e:.3e}, vs single call {rel_err(Y, single):.3e}",
+              flush=True)
+        assert e <= tol
+        assert rel_err(Y, single) <= tol
+
+
+def test_q4k_group_ragged_members(hip, oracle_mod):
+    """Members whose row counts are not multiples of 16 (tile padding inside the group)."""
+    from tests.gpu_util import q4k_matmul_group
+    in_, outs = 512, [17, 33, 100, 1]
+    raws = [synth.q4k_weights(o, in_, seed=500 + i) for i, o in enumerate(outs)]
+    X = synth.activations(2, in_, seed=599)
+    Ys = q4k_matmul_group(raws, outs, in_, X, 2)
+    for raw, o, Y in zip(raws, outs, Ys):
+        assert rel_err(Y, oracle_mod.q4k_gemm(raw, o, in_, X, 2)) <= GEMV_TOL
