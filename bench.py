@@ -261,6 +261,41 @@ def bench_small_m(steps, warmup, ev):
     return out
 
 
+def decode_graph_ms(calls, steps, warmup, ev):
+    """One token's calls captured once as a graph (fhip_graph_*) on a created stream and
+    replayed: ms per replay."""
+    lib = fakhip.load()
+    st = C.c_void_p()
+    fakhip.call("fhip_stream_create", C.byref(st))
+    fakhip.call("fhip_set_stream", st)
+    graph = C.c_void_p()
+    try:
+        def run():
+            for fn, args in calls:
+                rc = getattr(lib, fn)(*args(0))
+                if rc:
+                    fakhip.check(fn, rc)
+        run()  # eager: sizes the workspace before capture
+        fakhip.call("fhip_stream_sync", st)
+        fakhip.call("fhip_graph_begin")
+        run()
+        fakhip.call("fhip_graph_end", C.byref(graph))
+        for _ in range(warmup):
+            fakhip.call("fhip_graph_launch", graph)
+        fakhip.call("fhip_stream_sync", st)
+        a, b = ev.new(), ev.new()
+        ev.record(a)
+        for _ in range(steps):
+            fakhip.call("fhip_graph_launch", graph)
+        ev.record(b)
+        return ev.ms(a, b) / steps
+    finally:
+        if graph.value:
+            fakhip.call("fhip_graph_destroy", graph)
+        fakhip.call("fhip_set_stream", None)
+        fakhip.call("fhip_stream_destroy", st)
+
+
 def bench_decode_stack(steps, warmup, ev, layers=28):
     """C4: one token of a 28-layer Qwen2.5-7B-shaped decode (q, k, v, o, gate, up, down per layer
     + lm_head), all Q4_K, every layer at its own device address."""
@@ -313,6 +348,7 @@ def bench_decode_stack(steps, warmup, ev, layers=28):
     gcalls.append(("fhip_q4k_matmul_f32",
                    lambda i: (head.ptrs[0], xs[H].ptr, ys[V].ptr, V, H, 1)))
     gms, _ = time_calls(gcalls, steps, warmup, ev)
+    graph_ms = decode_graph_ms(gcalls, steps, warmup, ev)
     wbytes = layers * sum(q4k_bytes(n, k) for n, k in layer_shapes) + q4k_bytes(V, H)
     abytes = layers * sum(4 * (n + k) for n, k in layer_shapes) + 4 * (V + H)
     for l in range(1, layers):
@@ -330,7 +366,11 @@ def bench_decode_stack(steps, warmup, ev, layers=28):
             "grouped_qkv_gateup": {"launches_per_token": len(gcalls), "ms_per_token": gms,
                                    "tok_per_s": 1e3 / gms,
                                    "pct_hbm_peak": 100.0 * (wbytes + abytes) / (gms * 1e6)
-                                   / HBM_PEAK_GBS}}
+                                   / HBM_PEAK_GBS},
+            "grouped_graph": {"graph_launches_per_token": 1, "ms_per_token": graph_ms,
+                              "tok_per_s": 1e3 / graph_ms,
+                              "pct_hbm_peak": 100.0 * (wbytes + abytes) / (graph_ms * 1e6)
+                              / HBM_PEAK_GBS}}
 
 
 def cpu_baseline(ws, xs, ys, budget_s=10.0):

@@ -1,5 +1,5 @@
 // common.hpp — shared plumbing of the fakhip C ABI: status codes, the current stream, the
-// grow-only device workspace and the self-resetting ticket counters used by split-K kernels.
+// grow-only device workspace.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -21,13 +21,10 @@ int hip_fail(hipError_t e, const char *what);
 // Clear the per-thread error message at the start of an entry point.
 void clear_error();
 
-// Device scratch owned by the library, grown on demand (never shrunk). A grow synchronizes
-// the device first, so memory in use by queued kernels is never freed underneath them.
-// Returns nullptr (and records the error) on failure.
+// Device scratch owned by the library, grown on demand. A grow allocates a new buffer and
+// keeps the old one (queued kernels and captured graphs may still use it). Returns nullptr
+// (and records the error) on failure.
 void *workspace(size_t bytes);
-// `n` zero-initialised 32-bit counters. Kernels that take a ticket from one of them reset it
-// to zero before they exit, so the counters stay zero between calls without any memset.
-unsigned *tickets(size_t n);
 
 // Device properties cached by fhip_init.
 int cu_count();

@@ -11,6 +11,7 @@
 #include <map>
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 #include "common.hpp"
 
@@ -30,8 +31,7 @@ size_t g_free_bytes = 0;
 
 void *g_ws = nullptr;
 size_t g_ws_bytes = 0;
-unsigned *g_tickets = nullptr;
-size_t g_tickets_n = 0;
+std::vector<void *> g_ws_retired;  // earlier, smaller workspaces (kept for captured graphs)
 
 size_t bucket(size_t n) {
   if (n <= 4096) return 4096;
@@ -64,39 +64,16 @@ void *workspace(size_t bytes) {
   if (bytes <= g_ws_bytes) return g_ws;
   size_t want = bytes + bytes / 4;
   if (want < (16u << 20)) want = 16u << 20;
-  if (g_ws) {
-    hipError_t e = hipDeviceSynchronize();
-    if (e != hipSuccess) { hip_fail(e, "workspace grow: hipDeviceSynchronize"); return nullptr; }
-    (void)hipFree(g_ws);
-    g_ws = nullptr;
-    g_ws_bytes = 0;
-  }
+  // A smaller workspace is retired, not freed: graphs captured earlier may still launch
+  // kernels that use it (the growth is geometric, so the retired total stays below the
+  // current size).
   void *p = nullptr;
   hipError_t e = hipMalloc(&p, want);
   if (e != hipSuccess) { hip_fail(e, "workspace: hipMalloc"); return nullptr; }
+  if (g_ws) g_ws_retired.push_back(g_ws);
   g_ws = p;
   g_ws_bytes = want;
   return g_ws;
-}
-
-unsigned *tickets(size_t n) {
-  if (n <= g_tickets_n) return g_tickets;
-  size_t want = n < 65536 ? 65536 : n;
-  if (g_tickets) {
-    hipError_t e = hipDeviceSynchronize();
-    if (e != hipSuccess) { hip_fail(e, "tickets grow: hipDeviceSynchronize"); return nullptr; }
-    (void)hipFree(g_tickets);
-    g_tickets = nullptr;
-    g_tickets_n = 0;
-  }
-  void *p = nullptr;
-  hipError_t e = hipMalloc(&p, want * sizeof(unsigned));
-  if (e != hipSuccess) { hip_fail(e, "tickets: hipMalloc"); return nullptr; }
-  e = hipMemset(p, 0, want * sizeof(unsigned));
-  if (e != hipSuccess) { hip_fail(e, "tickets: hipMemset"); (void)hipFree(p); return nullptr; }
-  g_tickets = (unsigned *)p;
-  g_tickets_n = want;
-  return g_tickets;
 }
 
 }  // namespace fhip
@@ -274,6 +251,43 @@ int fhip_set_stream(void *s) {
 int fhip_stream_sync(void *s) {
   clear_error();
   FHIP_CHECK(hipStreamSynchronize((hipStream_t)s));
+  return FHIP_OK;
+}
+
+int fhip_graph_begin(void) {
+  clear_error();
+  if (!g_stream)
+    return fail(FHIP_EINVAL, "fhip_graph_begin: capture needs a stream from fhip_stream_create "
+                             "made current with fhip_set_stream");
+  FHIP_CHECK(hipStreamBeginCapture(g_stream, hipStreamCaptureModeRelaxed));
+  return FHIP_OK;
+}
+
+int fhip_graph_end(void **graph) {
+  clear_error();
+  if (!graph) return fail(FHIP_EINVAL, "fhip_graph_end: null out pointer");
+  *graph = nullptr;
+  hipGraph_t g = nullptr;
+  FHIP_CHECK(hipStreamEndCapture(g_stream, &g));
+  hipGraphExec_t ex = nullptr;
+  const hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_fail(e, "fhip_graph_end: hipGraphInstantiate");
+  *graph = (void *)ex;
+  return FHIP_OK;
+}
+
+int fhip_graph_launch(void *graph) {
+  clear_error();
+  if (!graph) return fail(FHIP_EINVAL, "fhip_graph_launch: null graph");
+  FHIP_CHECK(hipGraphLaunch((hipGraphExec_t)graph, g_stream));
+  return FHIP_OK;
+}
+
+int fhip_graph_destroy(void *graph) {
+  clear_error();
+  if (!graph) return FHIP_OK;
+  FHIP_CHECK(hipGraphExecDestroy((hipGraphExec_t)graph));
   return FHIP_OK;
 }
 

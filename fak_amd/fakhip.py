@@ -50,6 +50,10 @@ SIGNATURES = {
     "fhip_stream_destroy": (_i, [_vp]),
     "fhip_set_stream": (_i, [_vp]),
     "fhip_stream_sync": (_i, [_vp]),
+    "fhip_graph_begin": (_i, []),
+    "fhip_graph_end": (_i, [C.POINTER(_vp)]),
+    "fhip_graph_launch": (_i, [_vp]),
+    "fhip_graph_destroy": (_i, [_vp]),
     "fhip_event_create": (_i, [C.POINTER(_vp)]),
     "fhip_event_destroy": (_i, [_vp]),
     "fhip_event_record": (_i, [_vp]),

@@ -74,6 +74,17 @@ int fhip_stream_destroy(void *stream);
 /* Make `stream` (NULL = the default stream) the target of every later launch and async copy. */
 int fhip_set_stream(void *stream);
 int fhip_stream_sync(void *stream);
+/* Graph capture of a sequence of calls (e.g. one decode token), the role of the reference's
+ * CUDA graph (internal/compute/cuda_kernels.cu:977-1043). Capture runs on the current stream,
+ * which must come from fhip_stream_create. Between begin and end only launch-only calls may be
+ * made: the *_matmul_f32 / *_group_f32 entries and fhip_q8_quantize_f32 (no fhip_malloc, no
+ * synchronous copies, no fhip_memset_async: memset nodes are not allowed in these graphs). Run
+ * each call once before capture so the library workspace already has its size. A graph replays
+ * the captured launches on the current stream with the same device pointers. */
+int fhip_graph_begin(void);
+int fhip_graph_end(void **graph);
+int fhip_graph_launch(void *graph);
+int fhip_graph_destroy(void *graph);
 int fhip_event_create(void **event);
 int fhip_event_destroy(void *event);
 /* Record on the current stream. */

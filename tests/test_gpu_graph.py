@@ -1,0 +1,94 @@
+"""Graph capture (fhip_graph_begin/end/launch): a captured sequence of matmul calls replays to the
+same bits as the same calls run eagerly, replay after replay, with new activation contents and
+eager work on the stream between replays (the way a decode loop reuses one captured token)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from fak_amd import fakhip, synth
+from tests.gpu_util import Dev
+
+pytestmark = pytest.mark.gpu
+
+
+def test_graph_replays_match_eager(hip):
+    print("[case] graph capture: q4k gemv/group/gemm, hal q8, gguf q8_0", flush=True)
+    lib = fakhip.load()
+    st = C.c_void_p()
+    fakhip.call("fhip_stream_create", C.byref(st))
+    fakhip.call("fhip_set_stream", st)
+    allocs, devs = [], []
+    try:
+        K = 1024
+        w1 = fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(1024, K, 11).ctypes.data, 1024, K)
+        wg = [fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(n, K, 12 + i).ctypes.data, n, K)
+              for i, n in enumerate((1024, 256, 256))]
+        w8 = fakhip.alloc_call("fhip_q8_0_upload", synth.q8_0_weights(512, K, 15).ctypes.data, 512, K)
+        allocs += [w1, w8] + wg
+        rng = np.random.default_rng(7)
+        codes = Dev.from_host(rng.integers(-127, 128, 320 * K, dtype=np.int8))
+        scales = Dev.from_host((np.abs(rng.standard_normal(320 * K // 32)) * 0.01).astype(np.float32))
+        x1 = Dev(K * 4)
+        x40 = Dev(40 * K * 4)
+        devs += [codes, scales, x1, x40]
+        outs = {name: (Dev(n * 4), Dev(n * 4)) for name, n in
+                [("gemv", 1024), ("g0", 1024), ("g1", 256), ("g2", 256), ("gemm", 40 * 1024),
+                 ("q8", 320), ("q8b", 4 * 320), ("gguf", 512)]}
+        for a, b in outs.values():
+            devs += [a, b]
+        outs_all = list(outs.keys())
+        gy = (C.c_void_p * 3)()
+        gw = (C.c_void_p * 3)(*wg)
+        gn = (C.c_int * 3)(1024, 256, 256)
+
+        def run(k):  # k = 0: the buffers the graph writes; 1: the eager check buffers
+            fakhip.call("fhip_q4k_matmul_f32", w1, x1.ptr, outs["gemv"][k].ptr, 1024, K, 1)
+            for i, nm in enumerate(("g0", "g1", "g2")):
+                gy[i] = outs[nm][k].ptr
+            fakhip.call("fhip_q4k_matmul_group_f32", C.addressof(gw), C.addressof(gy),
+                        C.addressof(gn), 3, x1.ptr, K, 1)
+            fakhip.call("fhip_q4k_matmul_f32", w1, x40.ptr, outs["gemm"][k].ptr, 1024, K, 40)
+            fakhip.call("fhip_q8_matmul_f32", codes.ptr, scales.ptr, x1.ptr, outs["q8"][k].ptr, 320,
+                        K, 1, 32)
+            fakhip.call("fhip_q8_matmul_f32", codes.ptr, scales.ptr, x40.ptr, outs["q8b"][k].ptr,
+                        320, K, 4, 32)
+            fakhip.call("fhip_q8_0_matmul_f32", w8, x1.ptr, outs["gguf"][k].ptr, 512, K, 1)
+
+        def set_x(seed):
+            fakhip.call("fhip_h2d", x1.ptr, synth.activations(1, K, seed).ctypes.data, K * 4)
+            fakhip.call("fhip_h2d", x40.ptr, synth.activations(40, K, seed + 1).ctypes.data,
+                        40 * K * 4)
+
+        set_x(100)
+        run(0)  # eager warm-up: sizes the workspace before capture
+        fakhip.call("fhip_sync")
+        fakhip.call("fhip_graph_begin")
+        run(0)
+        graph = C.c_void_p()
+        fakhip.call("fhip_graph_end", C.byref(graph))
+        try:
+            for rep in range(3):
+                set_x(200 + 10 * rep)
+                run(1)                      # eager work on the stream between replays
+                fakhip.call("fhip_graph_launch", graph)
+                fakhip.call("fhip_stream_sync", st)
+                for nm in outs_all:
+                    a, b = outs[nm]
+                    ga, eb = a.to_host(np.uint32), b.to_host(np.uint32)
+                    assert np.array_equal(ga, eb), (rep, nm)
+                print(f"    replay {rep}: all {len(outs_all)} outputs bit-identical", flush=True)
+        finally:
+            fakhip.call("fhip_graph_destroy", graph)
+    finally:
+        fakhip.call("fhip_set_stream", None)
+        for d in devs:
+            d.close()
+        for p in allocs:
+            lib.fhip_free(p)
+        fakhip.call("fhip_stream_destroy", st)
+
+
+def test_graph_begin_needs_a_created_stream(hip):
+    fakhip.call("fhip_set_stream", None)
+    assert fakhip.load().fhip_graph_begin() == -1
