@@ -26,6 +26,7 @@ from __future__ import annotations
 import ctypes as C
 import dataclasses
 import enum
+import os
 from typing import Optional
 
 import numpy as np
@@ -184,9 +185,14 @@ Q8_DEVICE_BLOCK = 32  # q8DeviceBlock, internal/compute/cuda.go:210
 class RocmBackend:
     """The ROCm (gfx950) Approx backend behind the compute.Backend seam."""
 
-    def __init__(self):
+    def __init__(self, kq_int8: Optional[bool] = None):
         self.info = fakhip.init()
         self._upload_cache: dict = {}
+        # The int8 Q4_K route is opt-in exactly as on the CPU: FAK_KQ_INT8 = 1 / on / true
+        # (q4kInt8Default, internal/model/quant_amd64_q4k.go:54-61), resolved once here.
+        if kq_int8 is None:
+            kq_int8 = os.environ.get("FAK_KQ_INT8", "") in ("1", "on", "true")
+        self.kq_int8 = bool(kq_int8)
 
     # ---- identity (compute.go:319-322) ----
     def Name(self) -> str:
@@ -336,7 +342,8 @@ class RocmBackend:
                              f"{P}x{in_}")
         y = self._dev_out(shape)
         if w.Dtype == Dtype.Q4_K:
-            fakhip.call("fhip_q4k_matmul_f32", w.buf.ptr, X.buf.ptr, y.buf.ptr, out, in_, P)
+            fn = "fhip_q4k_matmul_int8_f32" if self.kq_int8 else "fhip_q4k_matmul_f32"
+            fakhip.call(fn, w.buf.ptr, X.buf.ptr, y.buf.ptr, out, in_, P)
         elif w.Dtype == Dtype.Q8_0 and isinstance(w.buf, DevQ8Buf):
             fakhip.call("fhip_q8_matmul_f32", w.buf.ptr, w.buf.scales, X.buf.ptr, y.buf.ptr, out,
                         in_, P, w.buf.block)

@@ -18,23 +18,10 @@
 // written with __fmul_rn/__fsub_rn, which turned q8round of a product that rounds to 43.5 into 43
 // instead of 44.
 #include "kernels.hpp"
+#include "q8round.hpp"
 
 namespace fhip {
 namespace {
-
-// q8round (internal/model/quant.go:89-104): truncate toward zero, round the fraction half away
-// from zero, clamp to [-127, 127].
-__device__ __forceinline__ int q8round(float x) {
-  int t = (int)x;
-  const float f = __fsub_rn(x, (float)t);
-  if (f >= 0.5f)
-    t++;
-  else if (f <= -0.5f)
-    t--;
-  if (t > 127) return 127;
-  if (t < -127) return -127;
-  return t;
-}
 
 // One thread per (row, block): quantizeVecQ8 of X[rows][in] into codes [rows][in] and
 // scales [rows][in / block].

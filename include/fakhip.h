@@ -123,6 +123,14 @@ int fhip_q4k_matmul_f32(const void *dPacked, const float *dX, float *dY, int out
  * Each Y_i meets the fhip_q4k_matmul_f32 bound (not bit-identical to it: the K split may differ). */
 int fhip_q4k_matmul_group_f32(const void *const *dPacked, float *const *dY, const int *out,
                               int count, const float *dX, int in, int P);
+/* The int8 Q4_K route (FAK_KQ_INT8): Y[P,out] from a tiled Q4_K weight with every activation row
+ * quantized to int8 per 32 values — the replacement for q4kMatRowsInto / q4kGemmInto when
+ * q4kSDOTEnabled (internal/model/quant_q4k.go:125-136,190-218 -> q4kMatRowsRangeInt8,
+ * internal/model/quant_q4k_int8.go:135-142, and per token q4kGemmRangeInt8, quant_q4k.go:
+ * 359-372). Every value is bit-identical to that CPU route (quantizeRowQ8scalar, the int32
+ * sub-block sums, and q4kCombineRow's f32 chain in its order). dX must be 16-byte aligned. */
+int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, float *dY, int out, int in,
+                             int P);
 
 /* ---- Q8_0 (32-weight blocks of 34 B: f16 d + 32 int8; internal/ggufload/gguf.go:24) ----- */
 

@@ -50,6 +50,11 @@ def lib():
         L.fr_hal_q8_matmul.argtypes = [_i8p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
         L.fr_hal_q8_batched_matmul.argtypes = [_i8p, _f32p, _f32p, _f32p, C.c_int, C.c_int,
                                                C.c_int, C.c_int]
+        _i32p = C.POINTER(C.c_int32)
+        L.fr_q4k_reduce_row.argtypes = [_u8p, C.c_int, _i8p, _i32p, _i32p]
+        L.fr_q4k_combine_row.restype = C.c_float
+        L.fr_q4k_combine_row.argtypes = [_u8p, C.c_int, _f32p, _i32p, _i32p]
+        L.fr_q4k_matrows_int8.argtypes = [_u8p, C.c_int, C.c_int, _f32p, _f32p]
         for name in ("fr_q4k_matrows_par", "fr_q8_0_matrows_par"):
             fn = getattr(L, name)
             fn.restype = C.c_int
@@ -196,3 +201,47 @@ def hal_q8_batched_matmul(codes, scales, X, out: int, in_: int, P: int, block: i
     lib().fr_hal_q8_batched_matmul(_p(codes, _i8p), _p(scales, _f32p), _p(X, _f32p),
                                    _p(Y, _f32p), out, in_, P, block)
     return Y
+
+
+_i32p = C.POINTER(C.c_int32)
+
+
+def q4k_reduce_row(row: np.ndarray, nblk: int, qx: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """q4kReduceRowScalar, internal/model/quant_q4k_int8.go:72-100. Returns (IS, SS) int32."""
+    row = np.ascontiguousarray(row, np.uint8).reshape(-1)
+    qx = np.ascontiguousarray(qx, np.int8).reshape(-1)
+    assert row.size >= nblk * 144 and qx.size >= nblk * 256
+    IS = np.empty(nblk * 8, np.int32)
+    SS = np.empty(nblk * 8, np.int32)
+    lib().fr_q4k_reduce_row(_p(row, _u8p), nblk, _p(qx, _i8p), _p(IS, _i32p), _p(SS, _i32p))
+    return IS, SS
+
+
+def q4k_combine_row(row: np.ndarray, nblk: int, dx: np.ndarray, IS: np.ndarray,
+                    SS: np.ndarray) -> float:
+    """q4kCombineRow, internal/model/quant_q4k_int8.go:110-130."""
+    row = np.ascontiguousarray(row, np.uint8).reshape(-1)
+    dx = np.ascontiguousarray(dx, np.float32)
+    IS = np.ascontiguousarray(IS, np.int32)
+    SS = np.ascontiguousarray(SS, np.int32)
+    return float(lib().fr_q4k_combine_row(_p(row, _u8p), nblk, _p(dx, _f32p), _p(IS, _i32p),
+                                          _p(SS, _i32p)))
+
+
+def q4k_matrows_int8(raw: np.ndarray, out: int, in_: int, x: np.ndarray) -> np.ndarray:
+    """q4kMatRowsInto with q4kSDOTEnabled (FAK_KQ_INT8): quantizeVecQ8 once, then
+    q4kMatRowsRangeInt8, internal/model/quant_q4k.go:125-136 + quant_q4k_int8.go:135-142."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert in_ % 256 == 0 and raw.size == out * (in_ // 256) * 144 and x.size == in_
+    y = np.empty(out, np.float32)
+    lib().fr_q4k_matrows_int8(_p(raw, _u8p), out, in_, _p(x, _f32p), _p(y, _f32p))
+    return y
+
+
+def q4k_gemm_int8(raw: np.ndarray, out: int, in_: int, X: np.ndarray, P: int) -> np.ndarray:
+    """q4kGemmInto with q4kSDOTEnabled on amd64 (no extract-once): every token quantized on its
+    own and run through the int8 GEMV, internal/model/quant_q4k.go:190-218,359-372."""
+    X = np.ascontiguousarray(X, dtype=np.float32).reshape(P, in_)
+    return np.stack([q4k_matrows_int8(raw, out, in_, X[t]) for t in range(P)]) if P else \
+        np.empty((0, out), np.float32)

@@ -167,13 +167,17 @@ void fr_q8_0_matrows_range(const uint8_t *raw, int out, int in, const float *x, 
 }
 
 /* internal/compute/cpuref.go:486-501 */
+static inline float absf_(float v) { return v < 0 ? -v : v; }
+
 int8_t fr_q8round(float x) {
-  int32_t t = (int32_t)x; /* truncate toward zero */
+  /* truncate toward zero; NaN and |x| >= 2^31 give amd64's CVTTSS2SI "integer indefinite", and
+   * Go's int32 increment/decrement wrap (so -3e9 ends at +127) */
+  int32_t t = absf_(x) < 2147483648.f ? (int32_t)x : INT32_MIN;
   float f = x - (float)t;
   if (f >= 0.5f)
-    t++;
+    t = (int32_t)((uint32_t)t + 1u);
   else if (f <= -0.5f)
-    t--;
+    t = (int32_t)((uint32_t)t - 1u);
   if (t > 127) return 127;
   if (t < -127) return -127;
   return (int8_t)t;
@@ -270,6 +274,80 @@ void fr_hal_q8_batched_matmul(const int8_t *codes, const float *scales, const fl
                         dx + (size_t)t * nblk, nblk, block);
   free(qx);
   free(dx);
+}
+
+/* ---- the int8 Q4_K decode route (FAK_KQ_INT8), internal/model/quant_q4k_int8.go --------- */
+
+/* internal/model/quant_q4k_int8.go:72-100: per sub-block s of super-block b,
+ * IS[b*8+s] = sum(nibble * qx), SS[b*8+s] = sum(qx) over the sub-block's 32 values (int32). */
+void fr_q4k_reduce_row(const uint8_t *row, int nblk, const int8_t *qx, int32_t *IS, int32_t *SS) {
+  for (int b = 0; b < nblk; b++) {
+    const uint8_t *q = row + (size_t)b * Q4K_BLOCK_BYTES + 16;
+    const int base = b * 8;
+    int qi = 0;
+    for (int k = 0; k < 4; k++) {
+      const int8_t *qxA = qx + (size_t)(base + 2 * k) * 32;
+      int32_t IA = 0, SA = 0;
+      for (int l = 0; l < 32; l++) {
+        IA += (int32_t)(q[qi + l] & 0x0f) * (int32_t)qxA[l];
+        SA += (int32_t)qxA[l];
+      }
+      IS[base + 2 * k] = IA;
+      SS[base + 2 * k] = SA;
+      const int8_t *qxB = qx + (size_t)(base + 2 * k + 1) * 32;
+      int32_t IB = 0, SB = 0;
+      for (int l = 0; l < 32; l++) {
+        IB += (int32_t)(q[qi + l] >> 4) * (int32_t)qxB[l];
+        SB += (int32_t)qxB[l];
+      }
+      IS[base + 2 * k + 1] = IB;
+      SS[base + 2 * k + 1] = SB;
+      qi += 32;
+    }
+  }
+}
+
+/* internal/model/quant_q4k_int8.go:110-130: acc += (f32(I)*ws)*dxs; acc -= (f32(S)*wm)*dxs,
+ * ws = d*f32(sc), wm = min*f32(m), sub-block 0..7 within each super-block, blocks in order. */
+float fr_q4k_combine_row(const uint8_t *row, int nblk, const float *dx, const int32_t *IS,
+                         const int32_t *SS) {
+  float acc = 0;
+  for (int b = 0; b < nblk; b++) {
+    const uint8_t *blk = row + (size_t)b * Q4K_BLOCK_BYTES;
+    const float d = bits_f32(fr_f16_bits_to_f32_bits(le16(blk + 0)));
+    const float mn = bits_f32(fr_f16_bits_to_f32_bits(le16(blk + 2)));
+    const int base = b * 8;
+    for (int s = 0; s < 8; s++) {
+      uint8_t sc, m;
+      fr_get_scale_min_k4(s, blk + 4, &sc, &m);
+      const float ws = d * (float)sc, wm = mn * (float)m;
+      const float dxs = dx[base + s];
+      acc += ((float)IS[base + s] * ws) * dxs;
+      acc -= ((float)SS[base + s] * wm) * dxs;
+    }
+  }
+  return acc;
+}
+
+/* internal/model/quant_q4k_int8.go:135-142 with the activation quantized once by
+ * quantizeRowQ8scalar (internal/model/quant_quantize.go:16-43, == fr_quantize_vec_q8, block 32):
+ * the int8 decode GEMV of one token. */
+void fr_q4k_matrows_int8(const uint8_t *raw, int out, int in, const float *x, float *y) {
+  const int nblk = in / QK_K;
+  int8_t *qx = (int8_t *)malloc((size_t)in + 1);
+  float *dx = (float *)malloc(sizeof(float) * ((size_t)in / 32 + 1));
+  int32_t *IS = (int32_t *)malloc(sizeof(int32_t) * ((size_t)nblk * 8 + 1));
+  int32_t *SS = (int32_t *)malloc(sizeof(int32_t) * ((size_t)nblk * 8 + 1));
+  fr_quantize_vec_q8(x, in, 32, qx, dx);
+  const size_t rb = (size_t)nblk * Q4K_BLOCK_BYTES;
+  for (int o = 0; o < out; o++) {
+    fr_q4k_reduce_row(raw + (size_t)o * rb, nblk, qx, IS, SS);
+    y[o] = fr_q4k_combine_row(raw + (size_t)o * rb, nblk, dx, IS, SS);
+  }
+  free(qx);
+  free(dx);
+  free(IS);
+  free(SS);
 }
 
 /* ---- row-parallel drivers: internal/model/parallel.go:266-330 ---------------------------- */

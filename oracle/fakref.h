@@ -26,6 +26,14 @@
  *   fr_quantize_vec_q8, fr_qdot8, fr_qgemm8cell
  *                             closed forms on integer-exact inputs; order-revealing cases
  *                                                                          -> pinned
+ *   fr_q4k_reduce_row         vs an independent vectorised numpy integer reduction (exact)
+ *                                                                          -> pinned
+ *   fr_q4k_combine_row, fr_q4k_matrows_int8
+ *                             closed form on integer-exact inputs (d=1, dmin=0, amax=127 ->
+ *                             dx=1, the sum is an exact integer); order-revealing cases whose
+ *                             sequential result differs from a reassociated one; bounded
+ *                             distance from fr_q4k_matrows_range (activation quantization)
+ *                                                                          -> pinned
  * The exact bits the Go compiler would produce for the same loops are not available (no Go
  * toolchain); equality is argued from identical operation order with no contraction.
  */
@@ -82,6 +90,12 @@ void fr_hal_q8_batched_matmul(const int8_t *codes, const float *scales, const fl
  * ceil(out / (workers*4)) sized chunks grabbed dynamically by `workers` threads. Each row is
  * computed by exactly one thread with the serial arithmetic, so results are bit-identical to
  * the serial *_range call for any worker count. Return 0 on success. */
+/* the int8 Q4_K decode route (FAK_KQ_INT8), internal/model/quant_q4k_int8.go:72-142 */
+void fr_q4k_reduce_row(const uint8_t *row, int nblk, const int8_t *qx, int32_t *IS, int32_t *SS);
+float fr_q4k_combine_row(const uint8_t *row, int nblk, const float *dx, const int32_t *IS,
+                         const int32_t *SS);
+void fr_q4k_matrows_int8(const uint8_t *raw, int out, int in, const float *x, float *y);
+
 int fr_q4k_matrows_par(const uint8_t *raw, int out, int in, const float *x, float *y,
                        int workers);
 int fr_q4k_gemm_par(const uint8_t *raw, int out, int in, const float *X, int P, float *Y,

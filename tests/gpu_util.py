@@ -66,6 +66,18 @@ def q4k_matmul(raw: np.ndarray, out: int, in_: int, X: np.ndarray, P: int) -> np
         lib.fhip_free(w)
 
 
+def q4k_matmul_int8(raw: np.ndarray, out: int, in_: int, X: np.ndarray, P: int) -> np.ndarray:
+    """Upload raw Q4_K, run the int8 route fhip_q4k_matmul_int8_f32 on X[P, in]."""
+    lib = fakhip.load()
+    w = fakhip.alloc_call("fhip_q4k_upload", np.ascontiguousarray(raw).ctypes.data, out, in_)
+    try:
+        with Dev.from_host(np.ascontiguousarray(X, np.float32)) as dx, Dev(P * out * 4) as dy:
+            fakhip.call("fhip_q4k_matmul_int8_f32", w, dx.ptr, dy.ptr, out, in_, P)
+            return dy.to_host(np.float32).reshape(P, out)
+    finally:
+        lib.fhip_free(w)
+
+
 def q8_0_matmul(raw: np.ndarray, out: int, in_: int, X: np.ndarray, P: int) -> np.ndarray:
     lib = fakhip.load()
     w = fakhip.alloc_call("fhip_q8_0_upload", np.ascontiguousarray(raw).ctypes.data, out, in_)
