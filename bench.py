@@ -261,6 +261,31 @@ def bench_small_m(steps, warmup, ev):
     return out
 
 
+def bench_int8_route(steps, warmup, ev):
+    """The int8 Q4_K route (FAK_KQ_INT8, bit-identical to the CPU int8 GEMV) on the 7B FFN
+    decode shapes at M = 1, and on gate/up at M = 16."""
+    out = []
+    shapes = [(18944, 3584), (3584, 18944)]
+    ws = [Weight("q4k", n, k, 40 + i, copies_for(q4k_bytes(n, k))) for i, (n, k) in enumerate(shapes)]
+    for M, which in ((1, (0, 1)), (16, (0,))):
+        for idx in which:
+            (n, k), w = shapes[idx], ws[idx]
+            X = synth.activations(M, k, 50 + M)
+            xb, yb = Buf(X.nbytes, X), Buf(M * n * 4)
+            call = ("fhip_q4k_matmul_int8_f32",
+                    lambda i, w=w, xb=xb, yb=yb, n=n, k=k, M=M:
+                    (w.ptrs[i % len(w.ptrs)], xb.ptr, yb.ptr, n, k, M))
+            us = 1e3 * time_one(call, steps, warmup, ev)
+            alg = q4k_bytes(n, k) + 4 * M * (n + k)
+            out.append({"M": M, "N": n, "K": k, "us_per_call": round(us, 3),
+                        "GBs": round(alg / (us * 1e3), 1),
+                        "pct_hbm_peak": round(100.0 * alg / (us * 1e3) / HBM_PEAK_GBS, 1)})
+            xb.free(), yb.free()
+    for w in ws:
+        w.free()
+    return out
+
+
 def decode_graph_ms(calls, steps, warmup, ev):
     """One token's calls captured once as a graph (fhip_graph_*) on a created stream and
     replayed: ms per replay."""
@@ -457,6 +482,7 @@ def main():
         wl["c3_prefill_gemm"] = [bench_gemm(M, steps, 3, ev) for M in (128, 512, 2048)]
         wl["c4_decode_stack"] = bench_decode_stack(max(5, args.steps // 20), 2, ev)
         wl["c5_small_m"] = bench_small_m(steps, 3, ev)
+        wl["int8_route"] = bench_int8_route(steps, 3, ev)
         line["workloads"] = wl
     print(json.dumps(line), flush=True)
 
