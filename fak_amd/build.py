@@ -36,6 +36,12 @@ NO_CONTRACT = {"q8_hal.hip", "q4k_layout.hip", "q4k_i8route.hip"}
 RESOURCE_REMARK = "kernel-resource-usage"
 
 
+# Kernels allowed a small, measured spill (mangled-name fragment -> bytes per lane): the
+# three-workgroups-per-CU prefill GEMM keeps one 16-byte staging value in scratch once per
+# super-block (measured faster than the spill-free two-workgroup form: 116 vs 131 us at M=512).
+SCRATCH_ALLOWED = {"q4k_gemm32_kernelILi1ELi3E": 32}
+
+
 def scratch_kernels(remarks: str) -> list[tuple[str, int]]:
     """(kernel, bytes/lane) for every kernel whose resource-usage remark reports scratch."""
     out, name = [], None
@@ -64,8 +70,9 @@ def _compile(src: str, verbose: bool) -> str:
     if msgs and verbose:
         print(msgs, flush=True)
     # Register spills to scratch memory cost these bandwidth-bound kernels far more than they
-    # save; every kernel must fit its registers.
-    spills = scratch_kernels(out)
+    # save; every kernel must fit its registers, except the few listed in SCRATCH_ALLOWED.
+    spills = [(k, n) for k, n in scratch_kernels(out)
+              if not any(pat in k and n <= cap for pat, cap in SCRATCH_ALLOWED.items())]
     if spills:
         raise RuntimeError(f"{src}: kernels use scratch memory (register spills): {spills}")
     return obj

@@ -39,12 +39,21 @@ struct GemvGroup {
 int q4k_gemv_group(const GemvGroup &g, const float *X, int K, int M);
 int q4k_gemv_wide(const void *W, const float *X, float *Y, int N, int K, int M);
 int q4k_gemm(const void *W, const float *X, float *Y, int N, int K, int M);
+int q4k_gemm32(const void *W, const float *X, float *Y, int N, int K, int M);
 int q8_0_gemv(const void *W, const float *X, float *Y, int N, int K, int M);
 
 // __builtin_amdgcn_sched_barrier mask: every instruction class except vector-memory ones may be
 // scheduled across (ALU 0x1, VALU 0x2, SALU 0x4, MFMA 0x8, LDS 0x80). Placed after a ring
 // refill, it keeps the refill loads where the source puts them.
 constexpr int kNoVmemAcross = 0x0;
+
+// gfx9 VOP3 instructions cannot encode literal constants, so (q & mask) | magic with literal
+// operands compiles to two instructions. Holding the constants in registers (opaque to constant
+// folding) lets each nibble pair become one v_and_or_b32.
+__device__ __forceinline__ uint32_t in_reg(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 
 // Read an integer tuning override from the environment (0 when unset).
 int env_int(const char *name);

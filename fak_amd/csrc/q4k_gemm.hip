@@ -19,8 +19,14 @@ namespace {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint32_t lo02(uint32_t q) { return (q & 0x000F000Fu) | 0x64006400u; }
-__device__ __forceinline__ uint32_t hi02(uint32_t q) { return (q & 0x00F000F0u) | 0x64006400u; }
+// Mask and magic constants held in registers (in_reg) so each (q & mask) | magic is one
+// v_and_or_b32.
+struct Magic {
+  uint32_t lo, hi, byte02, magic;
+};
+__device__ __forceinline__ Magic magic_consts() {
+  return Magic{in_reg(0x000F000Fu), in_reg(0x00F000F0u), in_reg(0x00FF00FFu), in_reg(0x64006400u)};
+}
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 __device__ __forceinline__ uint32_t as_u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 
@@ -31,7 +37,7 @@ struct RowScales {
   h2 m1e[2], m1o[2];
 };
 
-__device__ __forceinline__ RowScales row_scales(uint4 h) {
+__device__ __forceinline__ RowScales row_scales(uint4 h, const Magic &K) {
   const h2 k1024 = {(_Float16)1024.f, (_Float16)1024.f};
   const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xffffu));
   const _Float16 dm = __builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16));
@@ -42,21 +48,23 @@ __device__ __forceinline__ RowScales row_scales(uint4 h) {
   const h2 k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
   RowScales s;
   // (v & 0x00FF00FF) | 0x64006400 = (1024 + byte0, 1024 + byte2) exactly.
-  s.d1e[0] = (as_h2((scl & 0x00FF00FFu) | 0x64006400u) - k1024) * dd;
-  s.d1o[0] = (as_h2(((scl >> 8) & 0x00FF00FFu) | 0x64006400u) - k1024) * dd * k16;
-  s.d1e[1] = (as_h2((sch & 0x00FF00FFu) | 0x64006400u) - k1024) * dd;
-  s.d1o[1] = (as_h2(((sch >> 8) & 0x00FF00FFu) | 0x64006400u) - k1024) * dd * k16;
-  s.m1e[0] = (as_h2((mnl & 0x00FF00FFu) | 0x64006400u) - k1024) * mm;
-  s.m1o[0] = (as_h2(((mnl >> 8) & 0x00FF00FFu) | 0x64006400u) - k1024) * mm;
-  s.m1e[1] = (as_h2((mnh & 0x00FF00FFu) | 0x64006400u) - k1024) * mm;
-  s.m1o[1] = (as_h2(((mnh >> 8) & 0x00FF00FFu) | 0x64006400u) - k1024) * mm;
+  s.d1e[0] = (as_h2((scl & K.byte02) | K.magic) - k1024) * dd;
+  s.d1o[0] = (as_h2(((scl >> 8) & K.byte02) | K.magic) - k1024) * dd * k16;
+  s.d1e[1] = (as_h2((sch & K.byte02) | K.magic) - k1024) * dd;
+  s.d1o[1] = (as_h2(((sch >> 8) & K.byte02) | K.magic) - k1024) * dd * k16;
+  s.m1e[0] = (as_h2((mnl & K.byte02) | K.magic) - k1024) * mm;
+  s.m1o[0] = (as_h2(((mnl >> 8) & K.byte02) | K.magic) - k1024) * mm;
+  s.m1e[1] = (as_h2((mnh & K.byte02) | K.magic) - k1024) * mm;
+  s.m1o[1] = (as_h2(((mnh >> 8) & K.byte02) | K.magic) - k1024) * mm;
   return s;
 }
 
 // Dequantize chunk c (bytes 32c.. of the row's nibbles) of one row tile into the two f16 MFMA
 // weight operands: sub-block 2c (low nibbles) and 2c+1 (high nibbles).
 __device__ __forceinline__ void dequant_chunk(uint32_t x0, uint32_t x1, const RowScales &s, int c,
-                                              f16x8 &bl, f16x8 &bh) {
+                                              const Magic &K, f16x8 &bl, f16x8 &bh) {
+  auto lo02 = [&](uint32_t q) { return (q & K.lo) | K.magic; };
+  auto hi02 = [&](uint32_t q) { return (q & K.hi) | K.magic; };
   const h2 k1024 = {(_Float16)1024.f, (_Float16)1024.f};
   const int p = c >> 1, hsel = c & 1;
   const h2 de = s.d1e[p], dodd = s.d1o[p], me = s.m1e[p], mo = s.m1o[p];
@@ -79,11 +87,11 @@ __device__ __forceinline__ void dequant_chunk(uint32_t x0, uint32_t x1, const Ro
 
 // Workgroup = 4 waves over TM 16-token tiles x 16 row tiles; wave w owns row tiles 4w..4w+3
 // (its weights stay in its registers) and all four share the token tiles through LDS.
-template <int TM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TM <= 4 ? 2 : 1, TM <= 4 ? 2 : 1))) void
+template <int TM, int R, int WPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void
 q4k_gemm_kernel(const uint8_t *__restrict__ W, const uint4 *__restrict__ xa,
                 float *__restrict__ Y, int N, int M, int nblk, int ntiles, int MTG, int remap) {
-  constexpr int R = 4;              // row tiles per wave
+  // R: row tiles per wave; the workgroup's 4 waves cover 4 R row tiles
   constexpr int AU = TM * 2 * 64;   // uint4 operand units per stage (TM tiles x 2 slices x 64)
   constexpr int APT = AU / 256;     // per thread
   __shared__ uint4 As[2][AU];
@@ -96,9 +104,10 @@ q4k_gemm_kernel(const uint8_t *__restrict__ W, const uint4 *__restrict__ xa,
   if (remap) wg = (wg & 7) * (gridDim.x >> 3) + (wg >> 3);
   const int mg = wg % MTG, ng = wg / MTG;
   const int nslices = nblk * 8;
-  const int rt0 = ng * 16 + wave * R;
+  const int rt0 = ng * 4 * R + wave * R;
   const uint4 *xg = xa + (size_t)mg * TM * nslices * 64;  // this group's token tiles (padded)
 
+  const Magic K = magic_consts();
   f32x4 acc[TM][R];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -148,7 +157,7 @@ q4k_gemm_kernel(const uint8_t *__restrict__ W, const uint4 *__restrict__ xa,
   for (int b = 0; b < nblk; ++b) {
     RowScales rs[R];
 #pragma unroll
-    for (int j = 0; j < R; ++j) rs[j] = row_scales(h[j]);
+    for (int j = 0; j < R; ++j) rs[j] = row_scales(h[j], K);
     const bool more = b + 1 < nblk;
     if (more) load_h(b + 1, h);
 #pragma unroll
@@ -160,7 +169,7 @@ q4k_gemm_kernel(const uint8_t *__restrict__ W, const uint4 *__restrict__ xa,
       for (int j = 0; j < R; ++j) {
         const uint4 q = c < 2 ? qa[j] : qb[j];
         const uint32_t x0 = (c & 1) ? q.z : q.x, x1 = (c & 1) ? q.w : q.y;
-        dequant_chunk(x0, x1, rs[j], c, bl[j], bh[j]);
+        dequant_chunk(x0, x1, rs[j], c, K, bl[j], bh[j]);
       }
       if (more && c == 1) load_q(b + 1, 0, qa);
       if (more && c == 3) load_q(b + 1, 1, qb);
@@ -199,14 +208,14 @@ q4k_gemm_kernel(const uint8_t *__restrict__ W, const uint4 *__restrict__ xa,
   }
 }
 
-template <int TM>
+template <int TM, int R, int WPE>
 int launch_gemm(const uint8_t *W, const uint4 *xa, float *Y, int N, int M, int nblk) {
   const int ntiles = q4k_tiles(N), MTG = gemm_mt(M) / TM;
-  const int NTG = ceil_div(ntiles, 16);
+  const int NTG = ceil_div(ntiles, 4 * R);
   const int grid = MTG * NTG;
   // XCD-grouped order is opt-in (FAK_HIP_GEMM_REMAP=1): measured 2-20% slower on the C3 shapes.
   const int remap = (grid % 8 == 0 && env_int("FAK_HIP_GEMM_REMAP")) ? 1 : 0;
-  q4k_gemm_kernel<TM><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG, remap);
+  q4k_gemm_kernel<TM, R, WPE><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG, remap);
   FHIP_CHECK_LAUNCH("q4k_gemm_kernel");
   return FHIP_OK;
 }
@@ -214,18 +223,23 @@ int launch_gemm(const uint8_t *W, const uint4 *xa, float *Y, int N, int M, int n
 }  // namespace
 
 int q4k_gemm(const void *Wv, const float *X, float *Y, int N, int K, int M) {
+  if (!env_int("FAK_HIP_GEMM16")) return q4k_gemm32(Wv, X, Y, N, K, M);
   const uint8_t *W = (const uint8_t *)Wv;
   const int nblk = K / 256;
   uint4 *xa = (uint4 *)workspace(gemm_xa_bytes(M, K));
   if (!xa) return FHIP_ENOMEM;
   if (int rc = launch_gemm_xprep(X, M, K, xa)) return rc;
-  int tm = env_int("FAK_HIP_GEMM_TM");
-  if (tm == 0) tm = 4;
-  switch (tm) {
-    case 4: return launch_gemm<4>(W, xa, Y, N, M, nblk);
-    case 8: return launch_gemm<8>(W, xa, Y, N, M, nblk);
+  // Shape: TM*100 + R*10 + waves per SIMD. 4x2 tiles at 3 waves/SIMD fill the chip better for
+  // a few hundred tokens; 4x4 at 2 waves/SIMD reuses each activation tile more for long prompts.
+  int cfg = env_int("FAK_HIP_GEMM_CFG");
+  if (cfg == 0) cfg = M <= 1024 ? 423 : 442;
+  switch (cfg) {
+    case 442: return launch_gemm<4, 4, 2>(W, xa, Y, N, M, nblk);
+    case 841: return launch_gemm<8, 4, 1>(W, xa, Y, N, M, nblk);
+    case 423: return launch_gemm<4, 2, 3>(W, xa, Y, N, M, nblk);
+    case 822: return launch_gemm<8, 2, 2>(W, xa, Y, N, M, nblk);
   }
-  return fail(FHIP_EINVAL, "q4k_gemm: FAK_HIP_GEMM_TM=%d not in {4,8}", tm);
+  return fail(FHIP_EINVAL, "q4k_gemm: FAK_HIP_GEMM_CFG=%d is not a built shape", cfg);
 }
 
 }  // namespace fhip

@@ -28,14 +28,6 @@
 namespace fhip {
 namespace {
 
-// gfx9 VOP3 instructions cannot encode literal constants, so (q & mask) | magic with literal
-// operands compiles to two instructions. Holding the constants in registers (opaque to constant
-// folding) lets each nibble pair become one v_and_or_b32.
-__device__ __forceinline__ uint32_t in_reg(uint32_t x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
 template <int M, bool LX>
 __global__ __launch_bounds__((LX && M == 1) ? 1024 : 512) void q4k_gemv_kernel(
     const uint8_t *__restrict__ W, const float *__restrict__ X, const uint4 *__restrict__ xg,
