@@ -31,7 +31,7 @@ CXXFLAGS = [
 # Files whose results must be bit-identical to the reference's Go arithmetic, which never fuses
 # multiply-add on amd64: hipcc contracts a*b+c into fma by default (pragmas included), so these
 # are compiled with contraction off.
-NO_CONTRACT = {"q8_hal.hip", "q4k_layout.hip", "q4k_i8route.hip"}
+NO_CONTRACT = {"q8_hal.hip", "q4k_layout.hip", "q4k_i8route.hip", "q6k.hip"}
 
 RESOURCE_REMARK = "kernel-resource-usage"
 

@@ -2,6 +2,7 @@
 // (described in tiled.hpp), and the bit-exact device dequantizer used to prove the layout and
 // the f16/6-bit decoding reproduce q4kDequantSuperBlock (internal/model/quant_q4k.go:90-111).
 #include "common.hpp"
+#include "f16bits.hpp"
 #include "tiled.hpp"
 
 namespace fhip {
@@ -54,30 +55,6 @@ __global__ void q4k_unpack_kernel(uint8_t *__restrict__ raw, const uint8_t *__re
       *reinterpret_cast<uint2 *>(qs + 64 * L + 32 + 8 * g) = make_uint2(v.z, v.w);
     }
   }
-}
-
-// F16BitsToF32Bits (internal/model/quantbits.go:15-36) in integer arithmetic, so the result is
-// bit-identical for every input (subnormals renormalised, NaN payloads kept unquieted).
-__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
-  const uint32_t sign = (h & 0x8000u) << 16;
-  const uint32_t exp = (h >> 10) & 0x1fu;
-  uint32_t frac = h & 0x3ffu;
-  uint32_t bits;
-  if (exp == 0) {
-    if (frac == 0) {
-      bits = sign;
-    } else {
-      // Shift the leading 1 up to bit 10; each shift lowers the exponent by one from -14.
-      const int sh = __clz(frac) - 21;  // frac < 2^10: clz >= 22, sh >= 1
-      frac = (frac << sh) & 0x3ffu;
-      bits = sign | ((uint32_t)(127 - 14 - sh) << 23) | (frac << 13);
-    }
-  } else if (exp == 0x1f) {
-    bits = sign | 0x7f800000u | (frac << 13);
-  } else {
-    bits = sign | ((exp - 15 + 127) << 23) | (frac << 13);
-  }
-  return __uint_as_float(bits);
 }
 
 // GetScaleMinK4 (internal/model/quantbits.go:42-47).

@@ -132,6 +132,21 @@ int fhip_q4k_matmul_group_f32(const void *const *dPacked, float *const *dY, cons
 int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, float *dY, int out, int in,
                              int P);
 
+/* ---- Q6_K (256-weight super-blocks of 210 B; internal/model/quant_kquant.go:45,139-163) ---- */
+
+/* Bytes of a raw Q6_K weight [out][in] (in a multiple of 256); 0 for a bad shape. */
+size_t fhip_q6k_bytes(int out, int in);
+/* Copy raw GGUF Q6_K bytes to the device (kept in GGUF order): the resident-weight upload of
+ * quantizeKQuantFromRaw(kind Q6_K) (internal/model/quant_kquant.go:236-250). */
+void *fhip_q6k_upload(const uint8_t *hRaw, int out, int in);
+/* dW[out][in] = the dequantized weights, bit-identical to q6kDequantSuperBlock
+ * (internal/model/quant_kquant.go:139-163). Test hook. */
+int fhip_q6k_dequant_f32(float *dW, const void *dRaw, int out, int in);
+/* Y[P][out] = X[P][in] @ W^T for a resident Q6_K weight: the replacement for
+ * kQuantMatRowsInto(kind Q6_K) (internal/model/quant_kquant.go:188-232), whose f32 route
+ * dequantizes each super-block and dots it; bound max|dY|/RMS(Y) <= 1e-3. */
+int fhip_q6k_matmul_f32(const void *dRaw, const float *dX, float *dY, int out, int in, int P);
+
 /* ---- Q8_0 (32-weight blocks of 34 B: f16 d + 32 int8; internal/ggufload/gguf.go:24) ----- */
 
 size_t fhip_q8_0_packed_bytes(int out, int in);

@@ -55,6 +55,9 @@ def lib():
         L.fr_q4k_combine_row.restype = C.c_float
         L.fr_q4k_combine_row.argtypes = [_u8p, C.c_int, _f32p, _i32p, _i32p]
         L.fr_q4k_matrows_int8.argtypes = [_u8p, C.c_int, C.c_int, _f32p, _f32p]
+        L.fr_q6k_dequant_superblock.argtypes = [_f32p, _u8p]
+        L.fr_q6k_matrows_range.argtypes = [_u8p, C.c_int, C.c_int, _f32p, _f32p, C.c_int,
+                                           C.c_int]
         for name in ("fr_q4k_matrows_par", "fr_q8_0_matrows_par"):
             fn = getattr(L, name)
             fn.restype = C.c_int
@@ -244,4 +247,33 @@ def q4k_gemm_int8(raw: np.ndarray, out: int, in_: int, X: np.ndarray, P: int) ->
     own and run through the int8 GEMV, internal/model/quant_q4k.go:190-218,359-372."""
     X = np.ascontiguousarray(X, dtype=np.float32).reshape(P, in_)
     return np.stack([q4k_matrows_int8(raw, out, in_, X[t]) for t in range(P)]) if P else \
+        np.empty((0, out), np.float32)
+
+
+def q6k_dequant(raw: np.ndarray, out: int, in_: int) -> np.ndarray:
+    """Row-wise q6kDequantSuperBlock, internal/model/quant_kquant.go:139-163."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1)
+    nblk = in_ // 256
+    assert raw.size == out * nblk * 210
+    w = np.empty((out, in_), np.float32)
+    L = lib()
+    for b in range(out * nblk):
+        L.fr_q6k_dequant_superblock(_p(w.reshape(-1)[b * 256:], _f32p), _p(raw[b * 210:], _u8p))
+    return w
+
+
+def q6k_matrows(raw: np.ndarray, out: int, in_: int, x: np.ndarray) -> np.ndarray:
+    """kQuantMatRowsInto(kind Q6_K) f32 route, internal/model/quant_kquant.go:188-232."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert in_ % 256 == 0 and raw.size == out * (in_ // 256) * 210 and x.size == in_
+    y = np.empty(out, np.float32)
+    lib().fr_q6k_matrows_range(_p(raw, _u8p), out, in_, _p(x, _f32p), _p(y, _f32p), 0, out)
+    return y
+
+
+def q6k_gemm(raw: np.ndarray, out: int, in_: int, X: np.ndarray, P: int) -> np.ndarray:
+    """P tokens through the Q6_K GEMV, Y[P, out]."""
+    X = np.ascontiguousarray(X, dtype=np.float32).reshape(P, in_)
+    return np.stack([q6k_matrows(raw, out, in_, X[t]) for t in range(P)]) if P else \
         np.empty((0, out), np.float32)

@@ -18,6 +18,7 @@
 #define Q4K_BLOCK_BYTES 144 /* internal/model/quant_q4k.go:52 */
 #define Q8_0_BLOCK_WEIGHTS 32
 #define Q8_0_BLOCK_BYTES 34 /* internal/model/quant_kquant.go:48-49 */
+#define Q6K_BLOCK_BYTES 210 /* internal/model/quant_kquant.go:45: 128 + 64 + 16 + 2 */
 
 static inline float bits_f32(uint32_t u) {
   float f;
@@ -155,6 +156,57 @@ void fr_q8_0_matrows_range(const uint8_t *raw, int out, int in, const float *x, 
       const float *xs = x + (size_t)b * Q8_0_BLOCK_WEIGHTS;
       float s0 = 0, s1 = 0, s2 = 0, s3 = 0;
       for (int i = 0; i < Q8_0_BLOCK_WEIGHTS; i += 4) {
+        s0 += buf[i] * xs[i];
+        s1 += buf[i + 1] * xs[i + 1];
+        s2 += buf[i + 2] * xs[i + 2];
+        s3 += buf[i + 3] * xs[i + 3];
+      }
+      acc += (s0 + s1) + (s2 + s3);
+    }
+    y[o] = acc;
+  }
+}
+
+/* internal/model/quant_kquant.go:139-163 (q6kDequantSuperBlock): 210-byte super-block, ql[128]
+ * low nibbles, qh[64] high 2-bit pairs, 16 int8 scales, f16 d at byte 208;
+ * w = (d * f32(int8 scale)) * f32(q - 32). */
+void fr_q6k_dequant_superblock(float *dst, const uint8_t *blk) {
+  const uint8_t *ql = blk, *qh = blk + 128, *sc = blk + 192;
+  const float d = bits_f32(fr_f16_bits_to_f32_bits(le16(blk + Q6K_BLOCK_BYTES - 2)));
+  int qlOff = 0, qhOff = 0, scOff = 0;
+  for (int n = 0; n < QK_K; n += 128) {
+    for (int l = 0; l < 32; l++) {
+      const int is = l / 16;
+      const int8_t q1 = (int8_t)((ql[qlOff + l] & 0x0f) | (((qh[qhOff + l] >> 0) & 3) << 4)) - 32;
+      const int8_t q2 = (int8_t)((ql[qlOff + l + 32] & 0x0f) | (((qh[qhOff + l] >> 2) & 3) << 4)) - 32;
+      const int8_t q3 = (int8_t)((ql[qlOff + l] >> 4) | (((qh[qhOff + l] >> 4) & 3) << 4)) - 32;
+      const int8_t q4 = (int8_t)((ql[qlOff + l + 32] >> 4) | (((qh[qhOff + l] >> 6) & 3) << 4)) - 32;
+      dst[n + l + 0] = d * (float)(int8_t)sc[scOff + is + 0] * (float)q1;
+      dst[n + l + 32] = d * (float)(int8_t)sc[scOff + is + 2] * (float)q2;
+      dst[n + l + 64] = d * (float)(int8_t)sc[scOff + is + 4] * (float)q3;
+      dst[n + l + 96] = d * (float)(int8_t)sc[scOff + is + 6] * (float)q4;
+    }
+    qlOff += 64;
+    qhOff += 32;
+    scOff += 8;
+  }
+}
+
+/* internal/model/quant_kquant.go:210-232 with kind Q6_K (blockWeights 256, blockBytes 210) */
+void fr_q6k_matrows_range(const uint8_t *raw, int out, int in, const float *x, float *y, int lo,
+                          int hi) {
+  (void)out;
+  const int nblk = in / QK_K;
+  const size_t rowBytes = (size_t)nblk * Q6K_BLOCK_BYTES;
+  float buf[QK_K];
+  for (int o = lo; o < hi; o++) {
+    const uint8_t *row = raw + (size_t)o * rowBytes;
+    float acc = 0;
+    for (int b = 0; b < nblk; b++) {
+      fr_q6k_dequant_superblock(buf, row + (size_t)b * Q6K_BLOCK_BYTES);
+      const float *xs = x + (size_t)b * QK_K;
+      float s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+      for (int i = 0; i < QK_K; i += 4) {
         s0 += buf[i] * xs[i];
         s1 += buf[i + 1] * xs[i + 1];
         s2 += buf[i + 2] * xs[i + 2];

@@ -20,6 +20,13 @@
  *                             tolerance                                    -> pinned
  *   fr_q4k_gemm_range         == fr_q4k_matrows_range per token bitwise (the reference's own
  *                             invariant, prefill_q4k_test.go:75-110) + the above -> pinned
+ *   fr_q6k_dequant_superblock hand golden (quant_kquant_test.go:113-129: d=2, scales 1, codes 0
+ *                             -> -64); an index-revealing block whose every weight has its own
+ *                             (ql, qh, scale) combination, checked against an independent
+ *                             vectorised numpy decode of the GGUF Q6_K layout        -> pinned
+ *   fr_q6k_matrows_range      the reference's lcgBytes fixture (quant_kquant_test.go:51-88,
+ *                             d = 1, x = (7i % 23) - 11) = exact integer dot; order-revealing
+ *                             cancellation; f64 brute force                           -> pinned
  *   fr_q8_0_*                 hand golden (quant_kquant_test.go:154-167), integer-exact and
  *                             order-revealing fixtures                     -> pinned
  *   fr_q8round                vs round-half-away-from-zero over a dense sweep -> pinned
@@ -64,6 +71,11 @@ void fr_q4k_gemm_range(const uint8_t *raw, int out, int in, const float *X, int 
 
 /* internal/model/quant_iquant.go:14-19 */
 void fr_q8_0_dequant_block(float *dst, const uint8_t *blk);
+/* internal/model/quant_kquant.go:139-163 */
+void fr_q6k_dequant_superblock(float *dst, const uint8_t *blk);
+/* internal/model/quant_kquant.go:210-232 with kind Q6_K (blockWeights 256, blockBytes 210) */
+void fr_q6k_matrows_range(const uint8_t *raw, int out, int in, const float *x, float *y, int lo,
+                          int hi);
 /* internal/model/quant_kquant.go:210-232 with kind Q8_0 (blockWeights 32, blockBytes 34) */
 void fr_q8_0_matrows_range(const uint8_t *raw, int out, int in, const float *x, float *y,
                            int lo, int hi);

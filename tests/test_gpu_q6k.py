@@ -1,0 +1,83 @@
+"""GGUF Q6_K on the device (fhip_q6k_upload / fhip_q6k_dequant_f32 / fhip_q6k_matmul_f32)
+against the oracle's q6kDequantSuperBlock and kQuantMatRowsRange(kind Q6_K)
+(internal/model/quant_kquant.go:139-163,210-232): dequant bit-identical, the GEMV within
+max|dY|/RMS <= 1e-3 (exact on the reference's integer fixture)."""
+import numpy as np
+import pytest
+
+from fak_amd import fakhip
+from tests import q6k_cases as qc
+from tests.gpu_util import Dev, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def upload(raw, out, in_):
+    return fakhip.alloc_call("fhip_q6k_upload", np.ascontiguousarray(raw).ctypes.data, out, in_)
+
+
+def dev_dequant(raw, out, in_):
+    lib = fakhip.load()
+    w = upload(raw, out, in_)
+    try:
+        with Dev(out * in_ * 4) as dw:
+            fakhip.call("fhip_q6k_dequant_f32", dw.ptr, w, out, in_)
+            return dw.to_host(np.float32).reshape(out, in_)
+    finally:
+        lib.fhip_free(w)
+
+
+def dev_matmul(raw, out, in_, X, P):
+    lib = fakhip.load()
+    w = upload(raw, out, in_)
+    try:
+        with Dev.from_host(np.ascontiguousarray(X, np.float32)) as dx, Dev(P * out * 4) as dy:
+            fakhip.call("fhip_q6k_matmul_f32", w, dx.ptr, dy.ptr, out, in_, P)
+            return dy.to_host(np.float32).reshape(P, out)
+    finally:
+        lib.fhip_free(w)
+
+
+def test_dequant_bit_exact(hip, oracle_mod):
+    print("[case] q6k dequant: random blocks, every finite f16 exponent of d", flush=True)
+    rng = np.random.default_rng(3)
+    nb = 256
+    raw = rng.integers(0, 256, size=nb * 210, dtype=np.uint8).reshape(nb, 210)
+    d = (np.arange(nb, dtype=np.uint32) * 0x79 + 0x0401) & 0x7BFF  # spread over finite patterns
+    d[::7] |= 0x8000
+    d[5], d[6] = 0x0001, 0x03FF  # subnormals
+    raw[:, 208] = d & 0xFF
+    raw[:, 209] = d >> 8
+    got = dev_dequant(raw.reshape(-1), 1, nb * 256)
+    want = oracle_mod.q6k_dequant(raw.reshape(-1), 1, nb * 256)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_gemv_reference_fixture_exact(hip, oracle_mod):
+    raw, x, out, in_ = qc.reference_fixture()
+    y = dev_matmul(raw, out, in_, x, 1)[0]
+    np.testing.assert_array_equal(y, oracle_mod.q6k_matrows(raw, out, in_, x))
+
+
+@pytest.mark.parametrize("out,in_,P", [(1536, 3584, 1), (3584, 18944, 1), (152, 4096, 5),
+                                       (4096, 512, 3), (37, 256, 8)])
+def test_gemv_matches_oracle(hip, oracle_mod, out, in_, P):
+    print(f"[case] q6k gemv out={out} in={in_} P={P}", flush=True)
+    rng = np.random.default_rng(out + in_ + P)
+    raw = qc.pin_d(rng.integers(0, 256, size=out * (in_ // 256) * 210, dtype=np.uint8), 0x1400)
+    X = rng.standard_normal((P, in_)).astype(np.float32)
+    Y = dev_matmul(raw, out, in_, X, P)
+    ref = oracle_mod.q6k_gemm(raw, out, in_, X, P)
+    err = rel_err(Y, ref)
+    print(f"    max|d|/RMS = {err:.2e}", flush=True)
+    assert err <= 1e-3
+
+
+def test_argument_errors(hip):
+    lib = fakhip.load()
+    with Dev(4096) as a:
+        assert lib.fhip_q6k_matmul_f32(a.ptr, a.ptr, a.ptr, 4, 300, 1) == -1
+        assert lib.fhip_q6k_dequant_f32(a.ptr, a.ptr, 0, 256) == -1
+        assert lib.fhip_q6k_matmul_f32(a.ptr, a.ptr, a.ptr, 4, 256, 0) == 0
+    assert lib.fhip_q6k_bytes(3, 512) == 3 * 2 * 210
+    assert lib.fhip_q6k_bytes(3, 500) == 0
