@@ -286,6 +286,35 @@ def bench_int8_route(steps, warmup, ev):
     return out
 
 
+def bench_q6k(steps, warmup, ev):
+    """Raw GGUF Q6_K GEMV (the q4_k_m ffn_down / lm_head quant) on the 7B FFN shapes, M=1."""
+    out = []
+    for n, k in ((3584, 18944), (18944, 3584)):
+        rng = np.random.default_rng(n)
+        raw = rng.integers(0, 256, size=n * (k // 256) * 210, dtype=np.uint8).reshape(-1, 210)
+        raw[:, 208:210] = (np.abs(rng.standard_normal(raw.shape[0])) * 1e-3).astype(
+            np.float16).view(np.uint8).reshape(-1, 2)
+        nbytes = raw.size
+        lib = fakhip.load()
+        p0 = fakhip.alloc_call("fhip_q6k_upload", np.ascontiguousarray(raw).ctypes.data, n, k)
+        ptrs = [p0]
+        for _ in range(copies_for(nbytes) - 1):
+            p = fakhip.alloc_call("fhip_malloc", nbytes)
+            fakhip.call("fhip_d2d", p, p0, nbytes)
+            ptrs.append(p)
+        x = synth.activations(1, k, 5)
+        xb, yb = Buf(x.nbytes, x), Buf(n * 4)
+        call = ("fhip_q6k_matmul_f32", lambda i: (ptrs[i % len(ptrs)], xb.ptr, yb.ptr, n, k, 1))
+        us = 1e3 * time_one(call, steps, warmup, ev)
+        alg = nbytes + 4 * (n + k)
+        out.append({"N": n, "K": k, "us_per_call": round(us, 3), "GBs": round(alg / (us * 1e3), 1),
+                    "pct_hbm_peak": round(100.0 * alg / (us * 1e3) / HBM_PEAK_GBS, 1)})
+        xb.free(), yb.free()
+        for p in ptrs:
+            lib.fhip_free(p)
+    return out
+
+
 def decode_graph_ms(calls, steps, warmup, ev):
     """One token's calls captured once as a graph (fhip_graph_*) on a created stream and
     replayed: ms per replay."""
@@ -483,6 +512,7 @@ def main():
         wl["c4_decode_stack"] = bench_decode_stack(max(5, args.steps // 20), 2, ev)
         wl["c5_small_m"] = bench_small_m(steps, 3, ev)
         wl["int8_route"] = bench_int8_route(steps, 3, ev)
+        wl["q6k_gemv"] = bench_q6k(steps, 3, ev)
         line["workloads"] = wl
     print(json.dumps(line), flush=True)
 

@@ -2,7 +2,7 @@
 tokens, a number of repetitions, median-free plain timing with HIP events, and a one-line report.
 Used as the target program for rocprofv3 runs (kernel trace, counters) on one shape.
 
-    python -m fak_amd.q4kbench --n 18944 --k 3584 --m 1 --reps 20 [--q8]
+    python -m fak_amd.q4kbench --n 18944 --k 3584 --m 1 --reps 20 [--q8 | --q6k]
 
 Weights rotate over enough distinct device copies (> 256 MB) that the Infinity Cache cannot
 serve them.
@@ -23,11 +23,21 @@ def main() -> None:
     ap.add_argument("--m", type=int, default=1, help="tokens")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--q8", action="store_true", help="Q8_0 weights instead of Q4_K")
+    ap.add_argument("--q6k", action="store_true", help="raw Q6_K weights instead of Q4_K")
     ap.add_argument("--seed", type=int, default=1)
     a = ap.parse_args()
     fakhip.init()
     lib = fakhip.load()
-    if a.q8:
+    if a.q6k:
+        import numpy as np
+        rng = np.random.default_rng(a.seed)
+        raw = rng.integers(0, 256, size=a.n * (a.k // 256) * 210, dtype=np.uint8).reshape(-1, 210)
+        raw[:, 208:210] = (np.abs(rng.standard_normal(raw.shape[0])) * 1e-3).astype(
+            np.float16).view(np.uint8).reshape(-1, 2)
+        raw = raw.reshape(-1)
+        up, mm, nbytes = "fhip_q6k_upload", "fhip_q6k_matmul_f32", lib.fhip_q6k_bytes(a.n, a.k)
+        alg = nbytes
+    elif a.q8:
         raw = synth.q8_0_weights(a.n, a.k, a.seed)
         up, mm, nbytes = "fhip_q8_0_upload", "fhip_q8_0_matmul_f32", lib.fhip_q8_0_packed_bytes(a.n, a.k)
         alg = a.n * (a.k // 32) * 34
@@ -58,7 +68,7 @@ def main() -> None:
     fakhip.call("fhip_event_elapsed_ms", e0, e1, C.byref(ms))
     us = ms.value * 1e3 / a.reps
     bytes_ = alg + 4 * a.m * (a.n + a.k)
-    print(json.dumps({"n": a.n, "k": a.k, "m": a.m, "q8_0": a.q8, "reps": a.reps,
+    print(json.dumps({"n": a.n, "k": a.k, "m": a.m, "q8_0": a.q8, "q6_k": a.q6k, "reps": a.reps,
                       "us_per_call": round(us, 3), "GBs": round(bytes_ / us / 1e3, 1),
                       "TFLOPs": round(2.0 * a.m * a.n * a.k / us / 1e6, 2),
                       "weight_copies": len(ptrs)}), flush=True)
