@@ -30,6 +30,11 @@
 // its tiled weight records (tiled.hpp) exactly once with three 16-byte loads per lane, keeping
 // PF in flight; the KW partials of a tile are summed through LDS in part order
 // (deterministic).
+//
+// SwiGLU mode (the first stage of the fused decode MLP): the group is {gate, up} with tiles
+// interleaved (gate tile T, up tile T, gate tile T + 1, ...) and TW even, so both tiles of a row
+// block sit in one workgroup; the gate tile's final wave writes silu(gate) * up for its rows
+// instead of two separate outputs.
 #include "gemv_common.hpp"
 
 namespace fhip {
@@ -173,7 +178,13 @@ __device__ __forceinline__ void scale_min(uint32_t y, uint32_t z, uint32_t w, bo
   mn = (float)m;
 }
 
-template <int MP, bool LX>
+// silu(z) = z / (1 + e^-z) with e^-z evaluated in double and rounded to f32, the operation
+// order of internal/model/forward.go:452.
+__device__ __forceinline__ float silu_f32(float z) {
+  return z / (1.f + (float)exp(-(double)z));
+}
+
+template <int MP, bool LX, bool SWIGLU>
 __global__ __launch_bounds__(MP == 1 ? 1024 : 512) void q4k_gemv_i8_kernel(
     const GemvGroup grp, const float *__restrict__ X, const uint4 *__restrict__ xg, int K, int M,
     int nblk, int TW, int KW) {
@@ -187,8 +198,14 @@ __global__ __launch_bounds__(MP == 1 ? 1024 : 512) void q4k_gemv_i8_kernel(
   const int ntiles = grp.tile0[grp.count];
   const bool tvalid = Tg < ntiles;
   int mem = 0;  // the member this tile belongs to (wave-uniform scalar search)
-  while (mem + 1 < grp.count && Tg >= grp.tile0[mem + 1]) ++mem;
-  const int T = tvalid ? Tg - grp.tile0[mem] : 0;  // tile within the member
+  int T;        // tile within the member
+  if (SWIGLU) {
+    mem = Tg & 1;
+    T = tvalid ? Tg >> 1 : 0;
+  } else {
+    while (mem + 1 < grp.count && Tg >= grp.tile0[mem + 1]) ++mem;
+    T = tvalid ? Tg - grp.tile0[mem] : 0;
+  }
   const int N = grp.N[mem];
   float *__restrict__ Y = grp.Y[mem];
   const int b0 = (int)((long long)part * nblk / KW);
@@ -340,7 +357,8 @@ __global__ __launch_bounds__(MP == 1 ? 1024 : 512) void q4k_gemv_i8_kernel(
   for (int s = 0; s < NT; ++s) red[((tile * KW + part) * NT + s) * 64 + lane] = acc[s];
   __syncthreads();
   const int row = T * 16 + r;
-  if (part != 0 || !tvalid) return;
+  const bool fin = part == 0 && tvalid;
+  if (!SWIGLU && !fin) return;
   float v[NT];
 #pragma unroll
   for (int s = 0; s < NT; ++s) {
@@ -348,6 +366,24 @@ __global__ __launch_bounds__(MP == 1 ? 1024 : 512) void q4k_gemv_i8_kernel(
     for (int q = 1; q < KW; ++q) v[s] += red[((tile * KW + q) * NT + s) * 64 + lane];
     v[s] += __shfl_xor(v[s], 32);
     if (MP <= 2) v[s] += __shfl_xor(v[s], 16);
+  }
+  if (SWIGLU) {
+    // Every wave reaches this barrier; the up tile's final values go through LDS to its gate
+    // partner (tile + 1 holds up tile T when tile holds gate tile T).
+    float *xch = red + (size_t)blockDim.x / 64 * NT * 64;
+    if (fin)
+#pragma unroll
+      for (int s = 0; s < NT; ++s) xch[(tile * NT + s) * 64 + lane] = v[s];
+    __syncthreads();
+    if (!fin || mem != 0) return;
+    if (row < N && gq < (MP == 4 ? 2 : 1)) {
+#pragma unroll
+      for (int s = 0; s < NT; ++s) {
+        const int t = tok_of<MP>(gq, s);
+        if (t < M) Y[(size_t)t * N + row] = silu_f32(v[s]) * xch[((tile + 1) * NT + s) * 64 + lane];
+      }
+    }
+    return;
   }
   if (row < N && gq < (MP == 4 ? 2 : 1)) {
 #pragma unroll
@@ -417,42 +453,67 @@ void i8_shape(int ntiles, int nblk, int max_waves, size_t lds_fixed, size_t lds_
   while (TW > 1 && TW * KW > max_waves) TW--;
 }
 
+// swiglu: the group is {gate, up} with tile0[2] = 2 * tiles (interleaved; see the kernel).
+// xop: a caller-provided operand buffer for the global path (nullptr: the library workspace).
 template <int MP>
-int launch_i8(const GemvGroup &g, const float *X, int K, int M) {
+int launch_i8(const GemvGroup &g, const float *X, int K, int M, bool swiglu, void *xop) {
   constexpr int NT = MP == 1 ? 1 : 2;
   const int nblk = K / 256, ntiles = g.tile0[g.count];
   const int max_waves = MP == 1 ? 16 : 8;
   const size_t ldsx = (size_t)nblk * op_bytes<MP>();
   int TW, KW;
   i8_shape(ntiles, nblk, max_waves, ldsx, (size_t)64 * NT * 4, TW, KW);
-  const size_t redB = (size_t)TW * KW * 64 * NT * 4;
+  if (swiglu && (TW & 1)) {  // both tiles of a row block in one workgroup
+    if (TW > 1) {
+      TW -= 1;
+    } else {
+      TW = 2;
+      if (2 * KW > max_waves) KW = max_waves / 2;
+    }
+  }
+  const size_t redB = (size_t)TW * KW * 64 * NT * 4 + (swiglu ? (size_t)TW * 64 * NT * 4 : 0);
   const bool lds_x = !env_int("FAK_HIP_GEMV_GLOBALX") && ldsx + redB <= (size_t)lds_limit();
   const int grid = ceil_div(ntiles, TW), threads = 64 * TW * KW;
   if (lds_x) {
-    q4k_gemv_i8_kernel<MP, true><<<grid, threads, ldsx + redB, stream()>>>(g, X, nullptr, K, M,
-                                                                           nblk, TW, KW);
+    if (swiglu)
+      q4k_gemv_i8_kernel<MP, true, true><<<grid, threads, ldsx + redB, stream()>>>(
+          g, X, nullptr, K, M, nblk, TW, KW);
+    else
+      q4k_gemv_i8_kernel<MP, true, false><<<grid, threads, ldsx + redB, stream()>>>(
+          g, X, nullptr, K, M, nblk, TW, KW);
     FHIP_CHECK_LAUNCH("q4k_gemv_i8_kernel<lds>");
     return FHIP_OK;
   }
-  void *xop = workspace((size_t)nblk * op_bytes<MP>());
+  if (!xop) xop = workspace(gemv_i8_xop_bytes(K, M));
   if (!xop) return FHIP_ENOMEM;
   const int nprep = MP * nblk * 8;
   gemv_i8_prep_kernel<MP><<<ceil_div(nprep, 128), 128, 0, stream()>>>(X, K, M, nblk,
                                                                       (uint4 *)xop);
   FHIP_CHECK_LAUNCH("gemv_i8_prep_kernel");
-  q4k_gemv_i8_kernel<MP, false><<<grid, threads, redB, stream()>>>(g, X, (const uint4 *)xop, K,
-                                                                   M, nblk, TW, KW);
+  if (swiglu)
+    q4k_gemv_i8_kernel<MP, false, true><<<grid, threads, redB, stream()>>>(
+        g, X, (const uint4 *)xop, K, M, nblk, TW, KW);
+  else
+    q4k_gemv_i8_kernel<MP, false, false><<<grid, threads, redB, stream()>>>(
+        g, X, (const uint4 *)xop, K, M, nblk, TW, KW);
   FHIP_CHECK_LAUNCH("q4k_gemv_i8_kernel<global>");
   return FHIP_OK;
 }
 
-int launch_i8_any(const GemvGroup &g, const float *X, int K, int M) {
-  if (M == 1) return launch_i8<1>(g, X, K, M);
-  if (M == 2) return launch_i8<2>(g, X, K, M);
-  return launch_i8<4>(g, X, K, M);
+int launch_i8_any(const GemvGroup &g, const float *X, int K, int M, bool swiglu = false,
+                  void *xop = nullptr) {
+  if (M == 1) return launch_i8<1>(g, X, K, M, swiglu, xop);
+  if (M == 2) return launch_i8<2>(g, X, K, M, swiglu, xop);
+  return launch_i8<4>(g, X, K, M, swiglu, xop);
 }
 
 }  // namespace
+
+// Bytes of the global-path activation operands for K and 1..4 tokens.
+size_t gemv_i8_xop_bytes(int K, int M) {
+  const int nblk = K / 256;
+  return (size_t)nblk * (M == 1 ? op_bytes<1>() : M == 2 ? op_bytes<2>() : op_bytes<4>());
+}
 
 // Small-M entry: 1..4 tokens on the int8 kernel (FAK_HIP_GEMV_WIDE=1 forces the f16 one),
 // 5..16 on the f16 kernel of q4k_gemv_wide.hip.
@@ -479,6 +540,36 @@ int q4k_gemv_group(const GemvGroup &g, const float *X, int K, int M) {
     return FHIP_OK;
   }
   return launch_i8_any(g, X, K, M);
+}
+
+// The first stage of the fused decode MLP: inter[t][i] = silu(gate x_t)[i] * (up x_t)[i] for
+// 1..4 tokens in one launch. xop: operand buffer for the global path (gemv_i8_xop_bytes(K, M)).
+int q4k_gemv_swiglu(const void *gate, const void *up, const float *X, float *inter, int I, int K,
+                    int M, void *xop) {
+  if (M < 1 || M > 4) return fail(FHIP_EINVAL, "q4k_gemv_swiglu: M=%d outside 1..4", M);
+  GemvGroup g = {};
+  g.W[0] = (const uint8_t *)gate;
+  g.W[1] = (const uint8_t *)up;
+  g.Y[0] = g.Y[1] = inter;
+  g.N[0] = g.N[1] = I;
+  g.tile0[0] = 0;
+  g.tile0[1] = q4k_tiles(I);
+  g.tile0[2] = 2 * q4k_tiles(I);
+  g.count = 2;
+  return launch_i8_any(g, X, K, M, true, xop);
+}
+
+// A 1..4-token GEMV with a caller-provided global operand buffer (see q4k_gemv_swiglu).
+int q4k_gemv_ws(const void *W, const float *X, float *Y, int N, int K, int M, void *xop) {
+  if (M < 1 || M > 4) return fail(FHIP_EINVAL, "q4k_gemv_ws: M=%d outside 1..4", M);
+  GemvGroup g = {};
+  g.W[0] = (const uint8_t *)W;
+  g.Y[0] = Y;
+  g.N[0] = N;
+  g.tile0[0] = 0;
+  g.tile0[1] = q4k_tiles(N);
+  g.count = 1;
+  return launch_i8_any(g, X, K, M, false, xop);
 }
 
 }  // namespace fhip

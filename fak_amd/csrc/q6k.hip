@@ -95,6 +95,24 @@ int check_q6k_shape(const char *who, int out, int in) {
 }
 
 }  // namespace
+
+// Q6_K GEMV over any number of tokens, four per launch.
+int q6k_gemv(const void *dRaw, const float *dX, float *dY, int out, int in, int P) {
+  const unsigned grid = (unsigned)ceil_div(out, 4);
+  const uint8_t *W = (const uint8_t *)dRaw;
+  for (int t0 = 0; t0 < P; t0 += 4) {
+    const int mt = P - t0 < 4 ? P - t0 : 4;
+    switch (mt) {
+      case 1: q6k_gemv_kernel<1><<<grid, 256, 0, stream()>>>(W, dX, dY, out, in, t0); break;
+      case 2: q6k_gemv_kernel<2><<<grid, 256, 0, stream()>>>(W, dX, dY, out, in, t0); break;
+      case 3: q6k_gemv_kernel<3><<<grid, 256, 0, stream()>>>(W, dX, dY, out, in, t0); break;
+      default: q6k_gemv_kernel<4><<<grid, 256, 0, stream()>>>(W, dX, dY, out, in, t0); break;
+    }
+    FHIP_CHECK_LAUNCH("q6k_gemv_kernel");
+  }
+  return FHIP_OK;
+}
+
 }  // namespace fhip
 
 using namespace fhip;
@@ -137,19 +155,7 @@ int fhip_q6k_matmul_f32(const void *dRaw, const float *dX, float *dY, int out, i
   if (P < 0) return fail(FHIP_EINVAL, "fhip_q6k_matmul_f32: P=%d < 0", P);
   if (P == 0) return FHIP_OK;
   if (!dRaw || !dX || !dY) return fail(FHIP_EINVAL, "fhip_q6k_matmul_f32: null pointer");
-  const unsigned grid = (unsigned)ceil_div(out, 4);
-  const uint8_t *W = (const uint8_t *)dRaw;
-  for (int t0 = 0; t0 < P; t0 += 4) {
-    const int mt = P - t0 < 4 ? P - t0 : 4;
-    switch (mt) {
-      case 1: q6k_gemv_kernel<1><<<grid, 256, 0, stream()>>>(W, dX, dY, out, in, t0); break;
-      case 2: q6k_gemv_kernel<2><<<grid, 256, 0, stream()>>>(W, dX, dY, out, in, t0); break;
-      case 3: q6k_gemv_kernel<3><<<grid, 256, 0, stream()>>>(W, dX, dY, out, in, t0); break;
-      default: q6k_gemv_kernel<4><<<grid, 256, 0, stream()>>>(W, dX, dY, out, in, t0); break;
-    }
-    FHIP_CHECK_LAUNCH("q6k_gemv_kernel");
-  }
-  return FHIP_OK;
+  return q6k_gemv(dRaw, dX, dY, out, in, P);
 }
 
 }  // extern "C"

@@ -76,6 +76,8 @@ SIGNATURES = {
     "fhip_q6k_upload": (_vp, [_vp, _i, _i]),
     "fhip_q6k_dequant_f32": (_i, [_vp, _vp, _i, _i]),
     "fhip_q6k_matmul_f32": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "fhip_q4k_mlp_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
+    "fhip_q4k_mlp_q6down_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
     "fhip_q8_quantize_f32": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "fhip_q8_matmul_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i]),
 }

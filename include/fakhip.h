@@ -147,6 +147,24 @@ int fhip_q6k_dequant_f32(float *dW, const void *dRaw, int out, int in);
  * dequantizes each super-block and dots it; bound max|dY|/RMS(Y) <= 1e-3. */
 int fhip_q6k_matmul_f32(const void *dRaw, const float *dX, float *dY, int out, int in, int P);
 
+/* ---- Fused decode MLP (dense SwiGLU FFN of one decode step) ------------------------------- */
+
+/* Y[P][hidden] = down(silu(gate X) * (up X)) for P = 0..4 tokens, with silu(z) =
+ * z / (1 + f32(exp(f64(-z)))) (internal/model/forward.go:452). gate and up are tiled Q4_K
+ * [inter][hidden], down tiled Q4_K [hidden][inter]; hidden and inter multiples of 256. The
+ * replacement for mg_q4k_mlp (internal/metalgemm/q4k.m:458-520; FusedMLP,
+ * internal/metalgemm/q4k.go:144-161): two launches on the library stream, the intermediate stays
+ * on the device, no host synchronization. Each stage meets the GEMV bound; the output is within
+ * max|dY|/RMS(Y) <= 1e-3 of the CPU gate/up -> silu*up -> down chain (denseSwiGLU,
+ * internal/model/moe.go:111-136). dX and the weights 16-byte aligned. */
+int fhip_q4k_mlp_f32(const void *dGate, const void *dUp, const void *dDown, const float *dX,
+                     float *dY, int hidden, int inter, int P);
+/* The same with a raw Q6_K down projection (fhip_q6k_upload): the q4_k_m layout; the
+ * replacement for mg_q4k_mlp_q6down (internal/metalgemm/q4k.m:680-740; FusedMLPQ6Down,
+ * internal/metalgemm/q4k.go:180-205). */
+int fhip_q4k_mlp_q6down_f32(const void *dGate, const void *dUp, const void *dDownQ6,
+                            const float *dX, float *dY, int hidden, int inter, int P);
+
 /* ---- Q8_0 (32-weight blocks of 34 B: f16 d + 32 int8; internal/ggufload/gguf.go:24) ----- */
 
 size_t fhip_q8_0_packed_bytes(int out, int in);

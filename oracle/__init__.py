@@ -58,6 +58,9 @@ def lib():
         L.fr_q6k_dequant_superblock.argtypes = [_f32p, _u8p]
         L.fr_q6k_matrows_range.argtypes = [_u8p, C.c_int, C.c_int, _f32p, _f32p, C.c_int,
                                            C.c_int]
+        L.fr_silu.restype = C.c_float
+        L.fr_silu.argtypes = [C.c_float]
+        L.fr_swiglu.argtypes = [_f32p, _f32p, C.c_int]
         for name in ("fr_q4k_matrows_par", "fr_q8_0_matrows_par"):
             fn = getattr(L, name)
             fn.restype = C.c_int
@@ -277,3 +280,31 @@ def q6k_gemm(raw: np.ndarray, out: int, in_: int, X: np.ndarray, P: int) -> np.n
     X = np.ascontiguousarray(X, dtype=np.float32).reshape(P, in_)
     return np.stack([q6k_matrows(raw, out, in_, X[t]) for t in range(P)]) if P else \
         np.empty((0, out), np.float32)
+
+
+def silu(z: float) -> np.float32:
+    """internal/model/forward.go:452."""
+    return np.float32(lib().fr_silu(float(np.float32(z))))
+
+
+def swiglu(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """silu(g) * u elementwise (denseSwiGLU, internal/model/moe.go:111-136)."""
+    g = np.array(g, np.float32).reshape(-1)
+    u = np.ascontiguousarray(u, np.float32).reshape(-1)
+    assert g.size == u.size
+    lib().fr_swiglu(_p(g, _f32p), _p(u, _f32p), g.size)
+    return g
+
+
+def q4k_mlp(gate: np.ndarray, up: np.ndarray, down: np.ndarray, hidden: int, inter: int,
+            X: np.ndarray, P: int, down_q6: bool = False, workers: int = 1) -> np.ndarray:
+    """The dense SwiGLU FFN of a decode step on resident quantized weights (denseSwiGLU,
+    internal/model/moe.go:111-136): g = gate x, u = up x (Q4_K GEMV), g = silu(g) * u, then
+    y = down g (Q4_K, or Q6_K for the q4_k_m down projection), per token. Returns Y[P, hidden]."""
+    X = np.ascontiguousarray(X, np.float32).reshape(P, hidden)
+    G = q4k_gemm(gate, inter, hidden, X, P, workers)
+    U = q4k_gemm(up, inter, hidden, X, P, workers)
+    H = np.stack([swiglu(G[t], U[t]) for t in range(P)])
+    if down_q6:
+        return q6k_gemm(down, hidden, inter, H, P)
+    return q4k_gemm(down, hidden, inter, H, P, workers)

@@ -23,7 +23,7 @@ def build(verbose: bool = False) -> str:
     os.makedirs(OUT_DIR, exist_ok=True)
     src = os.path.join(HERE, "fakref.c")
     tmp = LIB + ".tmp%d" % os.getpid()
-    cmd = ["gcc", *CFLAGS, src, "-o", tmp]
+    cmd = ["gcc", *CFLAGS, src, "-o", tmp, "-lm"]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

@@ -9,6 +9,7 @@
  */
 #include "fakref.h"
 
+#include <math.h>
 #include <pthread.h>
 #include <stdatomic.h>
 #include <stdlib.h>
@@ -216,6 +217,15 @@ void fr_q6k_matrows_range(const uint8_t *raw, int out, int in, const float *x, f
     }
     y[o] = acc;
   }
+}
+
+/* internal/model/forward.go:452: z / (1 + float32(math.Exp(float64(-z)))) */
+float fr_silu(float z) { return z / (1.0f + (float)exp(-(double)z)); }
+
+/* the SwiGLU step of denseSwiGLU (internal/model/moe.go:111-136; the same loop as
+ * internal/model/profile.go:328): g[i] = silu(g[i]) * u[i] */
+void fr_swiglu(float *g, const float *u, int n) {
+  for (int i = 0; i < n; i++) g[i] = fr_silu(g[i]) * u[i];
 }
 
 /* internal/compute/cpuref.go:486-501 */

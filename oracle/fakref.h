@@ -41,6 +41,13 @@
  *                             sequential result differs from a reassociated one; bounded
  *                             distance from fr_q4k_matrows_range (activation quantization)
  *                                                                          -> pinned
+ *   fr_silu, fr_swiglu        special values (signed zeros, infinities, NaN, f32 overflow of
+ *                             e^-z) and an independent 50-digit decimal evaluation of
+ *                             e^-z rounded f64 -> f32, then 1 + t and z / s in IEEE f32 (numpy),
+ *                             bit-exact over a dense sweep. glibc's exp stands in for Go's
+ *                             math.Exp (both within 1 ulp in f64); the f32 rounding absorbs the
+ *                             difference except where e^-z lies within 1 f64 ulp of an f32
+ *                             rounding boundary                            -> pinned
  * The exact bits the Go compiler would produce for the same loops are not available (no Go
  * toolchain); equality is argued from identical operation order with no contraction.
  */
@@ -83,6 +90,10 @@ void fr_q8_0_matrows_range(const uint8_t *raw, int out, int in, const float *x, 
 /* The HAL Q8 lane (int8 codes + f32 per-block scales; the activation is quantized).
  * internal/compute/cpuref.go:486-501 (== internal/model/quant.go:89-104) */
 int8_t fr_q8round(float x);
+/* internal/model/forward.go:452 */
+float fr_silu(float z);
+/* g[i] = silu(g[i]) * u[i] (denseSwiGLU, internal/model/moe.go:111-136) */
+void fr_swiglu(float *g, const float *u, int n);
 /* internal/compute/cpuref.go:505-527 (== internal/model/quant_quantize.go:16-43) */
 void fr_quantize_vec_q8(const float *x, int n, int block, int8_t *q, float *d);
 /* internal/compute/cpuref.go:531-549 */
