@@ -315,6 +315,59 @@ def bench_q6k(steps, warmup, ev):
     return out
 
 
+def bench_mlp(steps, warmup, ev, H=3584, I=18944):
+    """The fused decode MLP (fhip_q4k_mlp_f32 / fhip_q4k_mlp_q6down_f32) at the Qwen2.5-7B FFN
+    shape, M=1, over rotating weight copies; beside it the same weights as a grouped gate/up
+    launch + down launch with no SwiGLU (the unfused matmul pair)."""
+    cp = copies_for(3 * q4k_bytes(I, H))
+    gate, up = Weight("q4k", I, H, 81, cp), Weight("q4k", I, H, 82, cp)
+    down = Weight("q4k", H, I, 83, cp)
+    rng = np.random.default_rng(84)
+    raw6 = rng.integers(0, 256, size=H * (I // 256) * 210, dtype=np.uint8).reshape(-1, 210)
+    raw6[:, 208:210] = (np.abs(rng.standard_normal(raw6.shape[0])) * 1e-3).astype(
+        np.float16).view(np.uint8).reshape(-1, 2)
+    q6bytes = raw6.size
+    lib = fakhip.load()
+    q6 = [fakhip.alloc_call("fhip_q6k_upload", np.ascontiguousarray(raw6).ctypes.data, H, I)]
+    for _ in range(cp - 1):
+        p = fakhip.alloc_call("fhip_malloc", q6bytes)
+        fakhip.call("fhip_d2d", p, q6[0], q6bytes)
+        q6.append(p)
+    xb, yb = Buf(H * 4, synth.activations(1, H, 85)[0]), Buf(H * 4)
+    g_y, u_y = Buf(I * 4), Buf(I * 4)
+    n = len(gate.ptrs)
+    mlp = ("fhip_q4k_mlp_f32", lambda i: (gate.ptrs[i % n], up.ptrs[i % n], down.ptrs[i % n],
+                                          xb.ptr, yb.ptr, H, I, 1))
+    mlp6 = ("fhip_q4k_mlp_q6down_f32", lambda i: (gate.ptrs[i % n], up.ptrs[i % n], q6[i % n],
+                                                  xb.ptr, yb.ptr, H, I, 1))
+    groups = [((C.c_void_p * 2)(gate.ptrs[j], up.ptrs[j]), (C.c_void_p * 2)(g_y.ptr, u_y.ptr),
+               (C.c_int * 2)(I, I)) for j in range(n)]
+    pair = [("fhip_q4k_matmul_group_f32",
+             lambda i: (C.addressof(groups[i % n][0]), C.addressof(groups[i % n][1]),
+                        C.addressof(groups[i % n][2]), 2, xb.ptr, H, 1)),
+            ("fhip_q4k_matmul_f32", lambda i: (down.ptrs[i % n], g_y.ptr, yb.ptr, H, I, 1))]
+    alg4 = 3 * q4k_bytes(I, H) + 4 * (2 * H)
+    alg6 = 2 * q4k_bytes(I, H) + q6bytes + 4 * (2 * H)
+    us4 = 1e3 * time_one(mlp, steps, warmup, ev)
+    us6 = 1e3 * time_one(mlp6, steps, warmup, ev)
+    ms_pair, per_pair = time_calls(pair, steps, warmup, ev)
+    for w in (gate, up, down):
+        w.free()
+    for p in q6:
+        lib.fhip_free(p)
+    for b in (xb, yb, g_y, u_y):
+        b.free()
+    gbs = lambda a, us: round(a / (us * 1e3), 1)
+    return {"hidden": H, "inter": I, "copies": n,
+            "q4k_down": {"us_per_call": round(us4, 3), "alg_bytes": alg4, "GBs": gbs(alg4, us4),
+                         "pct_hbm_peak": round(100 * alg4 / (us4 * 1e3) / HBM_PEAK_GBS, 1)},
+            "q6k_down": {"us_per_call": round(us6, 3), "alg_bytes": alg6, "GBs": gbs(alg6, us6),
+                         "pct_hbm_peak": round(100 * alg6 / (us6 * 1e3) / HBM_PEAK_GBS, 1)},
+            "unfused_group_plus_down": {"us_per_step": round(1e3 * ms_pair, 3),
+                                        "per_call_us": [round(1e3 * p, 3) for p in per_pair],
+                                        "GBs": gbs(alg4, 1e3 * ms_pair)}}
+
+
 def decode_graph_ms(calls, steps, warmup, ev):
     """One token's calls captured once as a graph (fhip_graph_*) on a created stream and
     replayed: ms per replay."""
@@ -513,6 +566,7 @@ def main():
         wl["c5_small_m"] = bench_small_m(steps, 3, ev)
         wl["int8_route"] = bench_int8_route(steps, 3, ev)
         wl["q6k_gemv"] = bench_q6k(steps, 3, ev)
+        wl["fused_mlp"] = bench_mlp(steps, 3, ev)
         line["workloads"] = wl
     print(json.dumps(line), flush=True)
 

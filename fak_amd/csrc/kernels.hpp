@@ -38,12 +38,13 @@ struct GemvGroup {
 };
 int q4k_gemv_group(const GemvGroup &g, const float *X, int K, int M);
 int q4k_gemv_wide(const void *W, const float *X, float *Y, int N, int K, int M);
-// Fused decode MLP pieces (1..4 tokens): the SwiGLU stage over {gate, up}, a GEMV with a
-// caller-provided operand buffer, that buffer's size, and the Q6_K GEMV.
-size_t gemv_i8_xop_bytes(int K, int M);
+// Fused decode MLP pieces (1..4 tokens): the workspace a small-M call over `ntiles` tiles
+// needs, the SwiGLU stage over {gate, up}, a GEMV on a caller-provided workspace, and the Q6_K
+// GEMV.
+size_t gemv_i8_ws_bytes(int ntiles, int K, int M, bool swiglu);
 int q4k_gemv_swiglu(const void *gate, const void *up, const float *X, float *inter, int I, int K,
-                    int M, void *xop);
-int q4k_gemv_ws(const void *W, const float *X, float *Y, int N, int K, int M, void *xop);
+                    int M, void *ws);
+int q4k_gemv_ws(const void *W, const float *X, float *Y, int N, int K, int M, void *ws);
 int q6k_gemv(const void *W, const float *X, float *Y, int N, int K, int M);
 int q4k_gemm(const void *W, const float *X, float *Y, int N, int K, int M);
 int q4k_gemm32(const void *W, const float *X, float *Y, int N, int K, int M);

@@ -30,14 +30,17 @@ int check_mlp(const char *who, const void *g, const void *u, const void *d, cons
   return FHIP_OK;
 }
 
-// Workspace: the intermediate [P][inter] (256-byte padded), then one operand buffer shared by
+// Workspace: the intermediate [P][inter] (256-byte padded), then one scratch area shared by
 // the two launches (stream-ordered).
 int run_mlp(const void *g, const void *u, const void *d, const float *dX, float *dY, int hidden,
             int inter, int P, bool q4_down) {
   const size_t interB = ((size_t)P * inter * 4 + 255) & ~(size_t)255;
-  size_t opB = gemv_i8_xop_bytes(hidden, P);
-  if (q4_down && gemv_i8_xop_bytes(inter, P) > opB) opB = gemv_i8_xop_bytes(inter, P);
-  unsigned char *ws = (unsigned char *)workspace(interB + opB);
+  size_t opB = gemv_i8_ws_bytes(2 * q4k_tiles(inter), hidden, P, true);
+  if (q4_down) {
+    const size_t dB = gemv_i8_ws_bytes(q4k_tiles(hidden), inter, P, false);
+    if (dB > opB) opB = dB;
+  }
+  unsigned char *ws = (unsigned char *)workspace(interB + opB + 256);
   if (!ws) return FHIP_ENOMEM;
   float *mid = (float *)ws;
   void *xop = ws + interB;

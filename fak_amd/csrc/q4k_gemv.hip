@@ -31,6 +31,13 @@
 // PF in flight; the KW partials of a tile are summed through LDS in part order
 // (deterministic).
 //
+// Split K across workgroups (SK > 1, for few tiles and long rows such as the 7B down
+// projection's 224 tiles x 74 super-blocks): workgroup (group of TW tiles, part p) covers
+// super-blocks [p nblk / SK, (p + 1) nblk / SK) and quantizes only those activations. Each
+// finished tile writes its partial to a global buffer, fences, and bumps the tile's counter; the
+// workgroup that arrives last sums the SK partials in part order (deterministic, whichever
+// arrives last), writes Y and resets the counter. Nothing waits on another workgroup.
+//
 // SwiGLU mode (the first stage of the fused decode MLP): the group is {gate, up} with tiles
 // interleaved (gate tile T, up tile T, gate tile T + 1, ...) and TW even, so both tiles of a row
 // block sit in one workgroup; the gate tile's final wave writes silu(gate) * up for its rows
@@ -184,17 +191,38 @@ __device__ __forceinline__ float silu_f32(float z) {
   return z / (1.f + (float)exp(-(double)z));
 }
 
+// Per-tile arrival counters of the split-K reduction. Zero at load; every use returns its counter
+// to zero (the last arriver resets it), so calls and graph replays find them clear.
+constexpr int kMaxSplitTiles = 4096;
+__device__ unsigned g_split_cnt[kMaxSplitTiles];
+
+// Weight records each wave keeps in flight (LDS path) and the widest workgroup (waves) for one
+// token. Measured at the 7B FFN shapes: an 8-record ring with 8-wave workgroups, the
+// activation loads issued ahead of the ring, and lane-parallel coalesced quantization were all
+// slower (11.9-12 us gate/up, 14.7-15.1 us down, against 10.6 and 13.8 us here).
+constexpr int kPF1 = 4, kMaxWaves1 = 16;
+
 template <int MP, bool LX, bool SWIGLU>
-__global__ __launch_bounds__(MP == 1 ? 1024 : 512) void q4k_gemv_i8_kernel(
+__global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_kernel(
     const GemvGroup grp, const float *__restrict__ X, const uint4 *__restrict__ xg, int K, int M,
-    int nblk, int TW, int KW) {
+    int nblk, int TW, int KW, int SK, float *part_buf) {
   constexpr int NT = MP == 1 ? 1 : 2;  // token slots per lane
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: SGPRs
   const int gq = lane >> 4, r = lane & 15;
   const int tile = wave / KW, part = wave - tile * KW;
-  const int Tg = blockIdx.x * TW + tile;  // tile of the concatenated group
+  // Tile group and K split of this workgroup, and its K range [kb0, kb1). Everything before
+  // the first weight loads delays the whole wave, so the unsplit case does no division here
+  // (and the products below stay in 32 bits: nblk * SK < 2^31).
+  int tgrp = blockIdx.x, sp = 0, kb0 = 0, kb1 = nblk;
+  if (SK > 1) {
+    tgrp = blockIdx.x / SK;
+    sp = blockIdx.x - tgrp * SK;
+    kb0 = sp * nblk / SK;
+    kb1 = (sp + 1) * nblk / SK;
+  }
+  const int Tg = tgrp * TW + tile;  // tile of the concatenated group
   const int ntiles = grp.tile0[grp.count];
   const bool tvalid = Tg < ntiles;
   int mem = 0;  // the member this tile belongs to (wave-uniform scalar search)
@@ -208,17 +236,22 @@ __global__ __launch_bounds__(MP == 1 ? 1024 : 512) void q4k_gemv_i8_kernel(
   }
   const int N = grp.N[mem];
   float *__restrict__ Y = grp.Y[mem];
-  const int b0 = (int)((long long)part * nblk / KW);
-  const int b1 = (int)((long long)(part + 1) * nblk / KW);
-  const int nb = b1 - b0;  // super-blocks of this wave's K part (>= 1: KW <= nblk)
+  // This wave's part [b0, b1) of the workgroup's K range.
+  const int nbk = kb1 - kb0;
+  const int b0 = kb0 + part * nbk / KW;
+  const int b1 = kb0 + (part + 1) * nbk / KW;
+  const int nb = b1 - b0;  // super-blocks of this wave's K part (>= 1: KW <= nblk / SK)
   const uint8_t *base = grp.W[mem] + (size_t)T * nblk * kQ4kRecord;
 
-  // Operands for all of K (slot = super-block index): in LDS, quantized once by the whole
-  // workgroup for its TW tiles, or the prepared global buffer.
+  // Operands of the workgroup's K range: in LDS (slot = super-block - kb0), quantized once by
+  // the whole workgroup for its TW tiles, or the prepared global buffer of all of K (slot =
+  // super-block). The LDS area holds ceil(nblk / SK) slots.
+  const int slot0 = LX ? kb0 : 0;
+  const int nslots = LX && SK > 1 ? (nblk + SK - 1) / SK : nblk;
   const unsigned char *opb = LX ? smem : reinterpret_cast<const unsigned char *>(xg);
   const uint4 *A = reinterpret_cast<const uint4 *>(opb);
-  const float2 *ES = reinterpret_cast<const float2 *>(opb + (size_t)nblk * MP * 1024);
-  float *red = reinterpret_cast<float *>(smem + (LX ? (size_t)nblk * op_bytes<MP>() : 0));
+  const float2 *ES = reinterpret_cast<const float2 *>(opb + (size_t)nslots * MP * 1024);
+  float *red = reinterpret_cast<float *>(smem + (LX ? (size_t)nslots * op_bytes<MP>() : 0));
 
   // A lane's operand row belongs to one chunk per result block; with one or two tokens the
   // lane loads only for the MFMA of that chunk.
@@ -251,14 +284,14 @@ __global__ __launch_bounds__(MP == 1 ? 1024 : 512) void q4k_gemv_i8_kernel(
 #pragma unroll
       for (int m = 0; m < 4; ++m)
         if (MP == 4 || lane_chunk(m * MP / 4) == m)
-          o.a[m] = __builtin_bit_cast(i32x4, A[a_index(b, m)]);
+          o.a[m] = __builtin_bit_cast(i32x4, A[a_index(b - slot0, m)]);
 #pragma unroll
       for (int blk = 0; blk < MP; ++blk)
-        o.es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b, blk)];
+        o.es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b - slot0, blk)];
     }
   };
 
-  constexpr int PF = LX ? 4 : 2;
+  constexpr int PF = LX ? (MP == 1 ? kPF1 : 4) : 2;
   Ops ring[PF];
 #pragma unroll
   for (int u = 0; u < PF; ++u) {
@@ -267,9 +300,9 @@ __global__ __launch_bounds__(MP == 1 ? 1024 : 512) void q4k_gemv_i8_kernel(
       for (int m = 0; m < 4; ++m) ring[u].a[m] = i32x4{0, 0, 0, 0};
     if (u < nb) load(b0 + u, ring[u]);
   }
-  // With the first records in flight, the workgroup quantizes the activations of all of K.
+  // With the first records in flight, the workgroup quantizes the activations of its K range.
   if (LX) {
-    quant_range<MP>(X, K, M, 0, nblk, const_cast<uint4 *>(A), const_cast<float2 *>(ES),
+    quant_range<MP>(X, K, M, kb0, nbk, const_cast<uint4 *>(A), const_cast<float2 *>(ES),
                     threadIdx.x, blockDim.x);
     __syncthreads();
   }
@@ -297,10 +330,10 @@ __global__ __launch_bounds__(MP == 1 ? 1024 : 512) void q4k_gemv_i8_kernel(
 #pragma unroll
         for (int m = 0; m < 4; ++m)
           if (MP == 4 || lane_chunk(m * MP / 4) == m)
-            areg[m] = __builtin_bit_cast(i32x4, A[a_index(b, m)]);
+            areg[m] = __builtin_bit_cast(i32x4, A[a_index(b - slot0, m)]);
 #pragma unroll
         for (int blk = 0; blk < MP; ++blk)
-          es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b, blk)];
+          es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b - slot0, blk)];
       } else {
 #pragma unroll
         for (int m = 0; m < 4; ++m) areg[m] = cur.a[m];
@@ -385,6 +418,39 @@ __global__ __launch_bounds__(MP == 1 ? 1024 : 512) void q4k_gemv_i8_kernel(
     }
     return;
   }
+  if (!SWIGLU && SK > 1) {
+    // Split-K: publish this part, then the last of the SK workgroups of the tile reduces.
+    // The partials and the counter are accessed only through device-scope (sc1) stores, loads
+    // and atomics, which are coherent across the XCDs' L2s, so no cache-wide writeback or
+    // invalidate is needed: the writer waits for its partial stores to complete before it
+    // arrives, and the last arriver loads the partials only after its arrival returned.
+    const bool wr = row < N && gq < (MP == 4 ? 2 : 1);
+    if (wr)
+#pragma unroll
+      for (int s = 0; s < NT; ++s)
+        __hip_atomic_store(&part_buf[((size_t)sp * ntiles + Tg) * 64 + r * 4 + tok_of<MP>(gq, s)],
+                           v[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // every partial store acknowledged
+    unsigned old = 0;
+    if (lane == 0)
+      old = __hip_atomic_fetch_add(&g_split_cnt[Tg], 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, 0);
+    if (old != (unsigned)(SK - 1)) return;
+    if (lane == 0)
+      __hip_atomic_store(&g_split_cnt[Tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (wr)
+#pragma unroll
+      for (int s = 0; s < NT; ++s) {
+        const int t = tok_of<MP>(gq, s);
+        float a = 0.f;
+        for (int q = 0; q < SK; ++q)
+          a += __hip_atomic_load(&part_buf[((size_t)q * ntiles + Tg) * 64 + r * 4 + t],
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t < M) Y[(size_t)t * N + row] = a;
+      }
+    return;
+  }
   if (row < N && gq < (MP == 4 ? 2 : 1)) {
 #pragma unroll
     for (int s = 0; s < NT; ++s) {
@@ -453,66 +519,99 @@ void i8_shape(int ntiles, int nblk, int max_waves, size_t lds_fixed, size_t lds_
   while (TW > 1 && TW * KW > max_waves) TW--;
 }
 
-// swiglu: the group is {gate, up} with tile0[2] = 2 * tiles (interleaved; see the kernel).
-// xop: a caller-provided operand buffer for the global path (nullptr: the library workspace).
+// Launch shape of one small-M call: TW tiles x KW waves per workgroup, SK K-splits across
+// workgroups, activations in LDS or in a prepared global buffer, and the workspace it needs
+// (global operands, then the split-K partials).
+struct I8Plan {
+  int TW, KW, SK;
+  bool lds_x;
+  size_t lds_bytes, xop_bytes, part_bytes;
+};
+
 template <int MP>
-int launch_i8(const GemvGroup &g, const float *X, int K, int M, bool swiglu, void *xop) {
+I8Plan plan_i8(int ntiles, int K, bool swiglu) {
   constexpr int NT = MP == 1 ? 1 : 2;
-  const int nblk = K / 256, ntiles = g.tile0[g.count];
-  const int max_waves = MP == 1 ? 16 : 8;
-  const size_t ldsx = (size_t)nblk * op_bytes<MP>();
-  int TW, KW;
-  i8_shape(ntiles, nblk, max_waves, ldsx, (size_t)64 * NT * 4, TW, KW);
-  if (swiglu && (TW & 1)) {  // both tiles of a row block in one workgroup
-    if (TW > 1) {
-      TW -= 1;
+  const int nblk = K / 256;
+  const int max_waves = MP == 1 ? kMaxWaves1 : 8;
+  I8Plan p{};
+  // Split K across workgroups only on request (FAK_HIP_GEMV_SK): measured on the 7B and 27B
+  // down projections it gains at most 5% and loses elsewhere.
+  p.SK = swiglu ? 1 : env_int("FAK_HIP_GEMV_SK");
+  if (p.SK <= 0) p.SK = 1;
+  if (p.SK > nblk) p.SK = nblk;
+  if (p.SK > 1 && ntiles > kMaxSplitTiles) p.SK = 1;
+  const int nbp = (nblk + p.SK - 1) / p.SK;  // super-blocks per split (at most)
+  const size_t ldsx = (size_t)nbp * op_bytes<MP>();
+  i8_shape(ntiles, nblk / p.SK, max_waves, ldsx, (size_t)64 * NT * 4, p.TW, p.KW);
+  if (p.KW > nblk / p.SK) p.KW = nblk / p.SK;
+  if (swiglu && (p.TW & 1)) {  // both tiles of a row block in one workgroup
+    if (p.TW > 1) {
+      p.TW -= 1;
     } else {
-      TW = 2;
-      if (2 * KW > max_waves) KW = max_waves / 2;
+      p.TW = 2;
+      if (2 * p.KW > max_waves) p.KW = max_waves / 2;
     }
   }
-  const size_t redB = (size_t)TW * KW * 64 * NT * 4 + (swiglu ? (size_t)TW * 64 * NT * 4 : 0);
-  const bool lds_x = !env_int("FAK_HIP_GEMV_GLOBALX") && ldsx + redB <= (size_t)lds_limit();
-  const int grid = ceil_div(ntiles, TW), threads = 64 * TW * KW;
-  if (lds_x) {
-    if (swiglu)
-      q4k_gemv_i8_kernel<MP, true, true><<<grid, threads, ldsx + redB, stream()>>>(
-          g, X, nullptr, K, M, nblk, TW, KW);
-    else
-      q4k_gemv_i8_kernel<MP, true, false><<<grid, threads, ldsx + redB, stream()>>>(
-          g, X, nullptr, K, M, nblk, TW, KW);
-    FHIP_CHECK_LAUNCH("q4k_gemv_i8_kernel<lds>");
-    return FHIP_OK;
+  const size_t redB =
+      (size_t)p.TW * p.KW * 64 * NT * 4 + (swiglu ? (size_t)p.TW * 64 * NT * 4 : 0);
+  p.lds_x = !env_int("FAK_HIP_GEMV_GLOBALX") && ldsx + redB <= (size_t)lds_limit();
+  p.lds_bytes = (p.lds_x ? ldsx : 0) + redB;
+  p.xop_bytes = p.lds_x ? 0 : (((size_t)nblk * op_bytes<MP>() + 255) & ~(size_t)255);
+  p.part_bytes = p.SK > 1 ? (size_t)p.SK * ntiles * 64 * 4 : 0;
+  return p;
+}
+
+// swiglu: the group is {gate, up} with tile0[2] = 2 * tiles (interleaved; see the kernel).
+// ws: a caller-provided workspace of plan_i8(...).xop_bytes + part_bytes (nullptr: the library
+// workspace).
+template <int MP>
+int launch_i8(const GemvGroup &g, const float *X, int K, int M, bool swiglu, void *ws) {
+  const int nblk = K / 256, ntiles = g.tile0[g.count];
+  const I8Plan p = plan_i8<MP>(ntiles, K, swiglu);
+  const size_t wsB = p.xop_bytes + p.part_bytes;
+  if (!ws && wsB) ws = workspace(wsB);
+  if (wsB && !ws) return FHIP_ENOMEM;
+  unsigned char *xop = (unsigned char *)ws;
+  float *part = p.part_bytes ? (float *)((unsigned char *)ws + p.xop_bytes) : nullptr;
+  const int grid = ceil_div(ntiles, p.TW) * p.SK, threads = 64 * p.TW * p.KW;
+  const uint4 *xg = nullptr;
+  if (!p.lds_x) {
+    const int nprep = MP * nblk * 8;
+    gemv_i8_prep_kernel<MP><<<ceil_div(nprep, 128), 128, 0, stream()>>>(X, K, M, nblk,
+                                                                        (uint4 *)xop);
+    FHIP_CHECK_LAUNCH("gemv_i8_prep_kernel");
+    xg = (const uint4 *)xop;
   }
-  if (!xop) xop = workspace(gemv_i8_xop_bytes(K, M));
-  if (!xop) return FHIP_ENOMEM;
-  const int nprep = MP * nblk * 8;
-  gemv_i8_prep_kernel<MP><<<ceil_div(nprep, 128), 128, 0, stream()>>>(X, K, M, nblk,
-                                                                      (uint4 *)xop);
-  FHIP_CHECK_LAUNCH("gemv_i8_prep_kernel");
-  if (swiglu)
-    q4k_gemv_i8_kernel<MP, false, true><<<grid, threads, redB, stream()>>>(
-        g, X, (const uint4 *)xop, K, M, nblk, TW, KW);
-  else
-    q4k_gemv_i8_kernel<MP, false, false><<<grid, threads, redB, stream()>>>(
-        g, X, (const uint4 *)xop, K, M, nblk, TW, KW);
-  FHIP_CHECK_LAUNCH("q4k_gemv_i8_kernel<global>");
+#define FHIP_I8_LAUNCH(LXV, SWV)                                                             \
+  q4k_gemv_i8_kernel<MP, LXV, SWV><<<grid, threads, p.lds_bytes, stream()>>>(              \
+      g, X, xg, K, M, nblk, p.TW, p.KW, p.SK, part)
+  if (p.lds_x) {
+    if (swiglu) FHIP_I8_LAUNCH(true, true);
+    else FHIP_I8_LAUNCH(true, false);
+  } else {
+    if (swiglu) FHIP_I8_LAUNCH(false, true);
+    else FHIP_I8_LAUNCH(false, false);
+  }
+#undef FHIP_I8_LAUNCH
+  FHIP_CHECK_LAUNCH("q4k_gemv_i8_kernel");
   return FHIP_OK;
 }
 
 int launch_i8_any(const GemvGroup &g, const float *X, int K, int M, bool swiglu = false,
-                  void *xop = nullptr) {
-  if (M == 1) return launch_i8<1>(g, X, K, M, swiglu, xop);
-  if (M == 2) return launch_i8<2>(g, X, K, M, swiglu, xop);
-  return launch_i8<4>(g, X, K, M, swiglu, xop);
+                  void *ws = nullptr) {
+  if (M == 1) return launch_i8<1>(g, X, K, M, swiglu, ws);
+  if (M == 2) return launch_i8<2>(g, X, K, M, swiglu, ws);
+  return launch_i8<4>(g, X, K, M, swiglu, ws);
 }
 
 }  // namespace
 
-// Bytes of the global-path activation operands for K and 1..4 tokens.
-size_t gemv_i8_xop_bytes(int K, int M) {
-  const int nblk = K / 256;
-  return (size_t)nblk * (M == 1 ? op_bytes<1>() : M == 2 ? op_bytes<2>() : op_bytes<4>());
+// Workspace bytes of a 1..4-token call over `ntiles` tiles with reduction dim K (see I8Plan).
+size_t gemv_i8_ws_bytes(int ntiles, int K, int M, bool swiglu) {
+  I8Plan p = M == 1 ? plan_i8<1>(ntiles, K, swiglu)
+           : M == 2 ? plan_i8<2>(ntiles, K, swiglu)
+                    : plan_i8<4>(ntiles, K, swiglu);
+  return p.xop_bytes + p.part_bytes;
 }
 
 // Small-M entry: 1..4 tokens on the int8 kernel (FAK_HIP_GEMV_WIDE=1 forces the f16 one),
@@ -543,9 +642,9 @@ int q4k_gemv_group(const GemvGroup &g, const float *X, int K, int M) {
 }
 
 // The first stage of the fused decode MLP: inter[t][i] = silu(gate x_t)[i] * (up x_t)[i] for
-// 1..4 tokens in one launch. xop: operand buffer for the global path (gemv_i8_xop_bytes(K, M)).
+// 1..4 tokens in one launch. ws: gemv_i8_ws_bytes(2 * q4k_tiles(I), K, M, true) bytes.
 int q4k_gemv_swiglu(const void *gate, const void *up, const float *X, float *inter, int I, int K,
-                    int M, void *xop) {
+                    int M, void *ws) {
   if (M < 1 || M > 4) return fail(FHIP_EINVAL, "q4k_gemv_swiglu: M=%d outside 1..4", M);
   GemvGroup g = {};
   g.W[0] = (const uint8_t *)gate;
@@ -556,11 +655,12 @@ int q4k_gemv_swiglu(const void *gate, const void *up, const float *X, float *int
   g.tile0[1] = q4k_tiles(I);
   g.tile0[2] = 2 * q4k_tiles(I);
   g.count = 2;
-  return launch_i8_any(g, X, K, M, true, xop);
+  return launch_i8_any(g, X, K, M, true, ws);
 }
 
-// A 1..4-token GEMV with a caller-provided global operand buffer (see q4k_gemv_swiglu).
-int q4k_gemv_ws(const void *W, const float *X, float *Y, int N, int K, int M, void *xop) {
+// A 1..4-token GEMV with a caller-provided workspace of gemv_i8_ws_bytes(q4k_tiles(N), K, M,
+// false) bytes.
+int q4k_gemv_ws(const void *W, const float *X, float *Y, int N, int K, int M, void *ws) {
   if (M < 1 || M > 4) return fail(FHIP_EINVAL, "q4k_gemv_ws: M=%d outside 1..4", M);
   GemvGroup g = {};
   g.W[0] = (const uint8_t *)W;
@@ -569,7 +669,7 @@ int q4k_gemv_ws(const void *W, const float *X, float *Y, int N, int K, int M, vo
   g.tile0[0] = 0;
   g.tile0[1] = q4k_tiles(N);
   g.count = 1;
-  return launch_i8_any(g, X, K, M, false, xop);
+  return launch_i8_any(g, X, K, M, false, ws);
 }
 
 }  // namespace fhip

@@ -55,6 +55,33 @@ def test_q4k_gemv_7b_ffn(hip, oracle_mod, out, in_):
     _check_q4k(oracle_mod, out, in_, 1, seed=2024 + out, tol=GEMV_TOL)
 
 
+@pytest.mark.parametrize("sk", [2, 3, 4, 8])
+@pytest.mark.parametrize("out,in_,P", [(33, 4096, 1), (100, 9472, 2), (3584, 18944, 1),
+                                       (40, 2048, 4), (7, 8192, 3)])
+def test_q4k_gemv_split_k(hip, oracle_mod, monkeypatch, sk, out, in_, P):
+    """K split across workgroups (FAK_HIP_GEMV_SK forces the split): ragged splits (37 super-
+    blocks over 3, 4, 8), one super-block per split, partial tiles, 1..4 tokens."""
+    monkeypatch.setenv("FAK_HIP_GEMV_SK", str(sk))
+    _check_q4k(oracle_mod, out, in_, P, seed=out + in_ + P + sk, tol=GEMV_TOL)
+
+
+def test_q4k_gemv_split_k_repeatable(hip, monkeypatch):
+    """The split-K reduction sums parts in a fixed order and resets its tile counters: repeated
+    calls (and calls with another split) give bit-identical results for the same split."""
+    out, in_ = 224 * 16, 74 * 256
+    raw = synth.q4k_weights(out, in_, seed=5)
+    X = synth.activations(1, in_, seed=6)
+    monkeypatch.setenv("FAK_HIP_GEMV_SK", "4")
+    a = q4k_matmul(raw, out, in_, X, 1)
+    b = q4k_matmul(raw, out, in_, X, 1)
+    monkeypatch.setenv("FAK_HIP_GEMV_SK", "2")
+    q4k_matmul(raw, out, in_, X, 1)
+    monkeypatch.setenv("FAK_HIP_GEMV_SK", "4")
+    c = q4k_matmul(raw, out, in_, X, 1)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+
+
 @pytest.mark.parametrize("P", [1, 4, 8, 16])
 @pytest.mark.parametrize("out,in_", [(25600, 5120), (5120, 25600)])
 def test_q4k_small_m_27b(hip, oracle_mod, out, in_, P):
