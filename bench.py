@@ -287,7 +287,7 @@ def bench_int8_route(steps, warmup, ev):
 
 
 def bench_q6k(steps, warmup, ev):
-    """Raw GGUF Q6_K GEMV (the q4_k_m ffn_down / lm_head quant) on the 7B FFN shapes, M=1."""
+    """GGUF Q6_K GEMV (the q4_k_m ffn_down / lm_head quant) on the 7B FFN shapes, M=1."""
     out = []
     for n, k in ((3584, 18944), (18944, 3584)):
         rng = np.random.default_rng(n)
@@ -298,9 +298,10 @@ def bench_q6k(steps, warmup, ev):
         lib = fakhip.load()
         p0 = fakhip.alloc_call("fhip_q6k_upload", np.ascontiguousarray(raw).ctypes.data, n, k)
         ptrs = [p0]
+        dev_bytes = lib.fhip_q6k_packed_bytes(n, k)
         for _ in range(copies_for(nbytes) - 1):
-            p = fakhip.alloc_call("fhip_malloc", nbytes)
-            fakhip.call("fhip_d2d", p, p0, nbytes)
+            p = fakhip.alloc_call("fhip_malloc", dev_bytes)
+            fakhip.call("fhip_d2d", p, p0, dev_bytes)
             ptrs.append(p)
         x = synth.activations(1, k, 5)
         xb, yb = Buf(x.nbytes, x), Buf(n * 4)
@@ -329,9 +330,10 @@ def bench_mlp(steps, warmup, ev, H=3584, I=18944):
     q6bytes = raw6.size
     lib = fakhip.load()
     q6 = [fakhip.alloc_call("fhip_q6k_upload", np.ascontiguousarray(raw6).ctypes.data, H, I)]
+    q6dev = lib.fhip_q6k_packed_bytes(H, I)
     for _ in range(cp - 1):
-        p = fakhip.alloc_call("fhip_malloc", q6bytes)
-        fakhip.call("fhip_d2d", p, q6[0], q6bytes)
+        p = fakhip.alloc_call("fhip_malloc", q6dev)
+        fakhip.call("fhip_d2d", p, q6[0], q6dev)
         q6.append(p)
     xb, yb = Buf(H * 4, synth.activations(1, H, 85)[0]), Buf(H * 4)
     g_y, u_y = Buf(I * 4), Buf(I * 4)

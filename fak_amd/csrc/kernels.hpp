@@ -63,6 +63,18 @@ __device__ __forceinline__ uint32_t in_reg(uint32_t x) {
   return x;
 }
 
+// Byte k of each of a, b, c, d, packed into one word (a in byte 0).
+__device__ __forceinline__ uint32_t pack_byte(int a, int b, int c, int d, int k) {
+  const uint32_t lo = 0x0c0c0000u | (uint32_t)(4 + k) << 8 | (uint32_t)k;  // 0x0c selects 0
+  const uint32_t hi = (uint32_t)(4 + k) << 24 | (uint32_t)k << 16 | 0x0c0cu;
+  return __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, lo) |
+         __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, hi);
+}
+
+// Workgroup shape of the small-M GEMV kernels (TW tiles x KW waves; see q4k_gemv.hip).
+void gemv_shape(int ntiles, int nblk, int max_waves, size_t lds_fixed, size_t lds_per_wave,
+                int &TW, int &KW);
+
 // Read an integer tuning override from the environment (0 when unset).
 int env_int(const char *name);
 

@@ -88,13 +88,6 @@ __host__ __device__ constexpr int es_of(int sig, int t) {
 template <int MP>
 __host__ __device__ constexpr size_t op_bytes() { return (size_t)MP * 1024 + (size_t)MP * 64; }
 
-// Byte k of each of a, b, c, d, packed into one word (a in byte 0).
-__device__ __forceinline__ uint32_t pack_byte(int a, int b, int c, int d, int k) {
-  const uint32_t lo = 0x0c0c0000u | (uint32_t)(4 + k) << 8 | (uint32_t)k;  // 0x0c selects 0
-  const uint32_t hi = (uint32_t)(4 + k) << 24 | (uint32_t)k << 16 | 0x0c0cu;
-  return __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, lo) |
-         __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, hi);
-}
 
 // Quantize one 32-value sub-block of one token (zeros when !valid) into the layout above.
 // A: operand entries of super-block slot bl; ES: its {e, S} pairs.
@@ -605,6 +598,11 @@ int launch_i8_any(const GemvGroup &g, const float *X, int K, int M, bool swiglu 
 }
 
 }  // namespace
+
+void gemv_shape(int ntiles, int nblk, int max_waves, size_t lds_fixed, size_t lds_per_wave,
+                int &TW, int &KW) {
+  i8_shape(ntiles, nblk, max_waves, lds_fixed, lds_per_wave, TW, KW);
+}
 
 // Workspace bytes of a 1..4-token call over `ntiles` tiles with reduction dim K (see I8Plan).
 size_t gemv_i8_ws_bytes(int ntiles, int K, int M, bool swiglu) {

@@ -19,6 +19,23 @@
 // The byte count is N_pad/16 * nblk * 2304 = N_pad * nblk * 144: the GGUF size, padded to 16
 // rows.
 //
+// Q6_K tiled layout. A weight [N][K/256] of 210-byte GGUF super-blocks (ql[128] | qh[64] |
+// int8 scales[16] | f16 d; internal/model/quant_kquant.go:139-163) is cut into tiles of 16 rows.
+// Tile T, super-block b becomes one 3360-byte record at byte ((T * nblk) + b) * 3360:
+//
+//   [0, 256)        row r's 16 scales at 16 r (dword c, byte g = scale of group 4c + g)
+//   [256, 288)      row r's f16 d at 256 + 2 r
+//   [288, 2336)     ql: half h, lane l = 16 g + r at 288 + 1024 h + 16 l: row r's ql bytes
+//                   [64 h + 16 g, +16)
+//   [2336, 3360)    qh: half h, g1 = g & 1 at 2336 + 512 h + 256 g1 + 16 r: row r's qh bytes
+//                   [32 h + 16 g1, +16)
+//
+// Weight 128 h + 32 i + l of a super-block (l < 32) is the low (i < 2) or high (i >= 2) nibble
+// of ql[64 h + 32 (i & 1) + l] with bits 2i..2i+1 of qh[32 h + l] above it, so the 16 weights
+// of group j = 8 h + 4 k + g (k = i >> 1 ... i = 2k + (g >> 1), l = 16 (g & 1) + pos) are the
+// nibble k of lane l's 16 ql bytes and the 2-bit field 4k + 2 (g >> 1) of its 16 qh bytes: one
+// 16-byte operand per lane and 16x16x64 MFMA. Rows past N are zero bytes (d = 0).
+//
 // Q8_0 tiled layout. A weight [N][K/32] of 34-byte blocks (f16 d + 32 int8; gguf.go:24) is cut
 // into tiles of 16 rows and pairs of blocks (64 weights). Record (T, pair) is 1088 bytes:
 //   [0, 64)         16 rows x 2 f16 scales (row r at 4*r).
@@ -48,6 +65,13 @@ inline int q4k_tiles(int out) { return ceil_div(out, kTileRows); }
 inline size_t q4k_packed_bytes(int out, int in) {
   return (size_t)q4k_tiles(out) * (size_t)(in / 256) * kQ4kRecord;
 }
+constexpr int kQ6kBlock = 210;
+constexpr int kQ6kRecord = 3360;  // 16 rows x 210 B
+constexpr int kQ6kD = 256, kQ6kQl = 288, kQ6kQh = 2336;
+inline size_t q6k_packed_bytes(int out, int in) {
+  return (size_t)q4k_tiles(out) * (size_t)(in / 256) * kQ6kRecord;
+}
+
 inline int q8_groups(int in) { return ceil_div(in / 32, kQ8Group); }
 inline size_t q8_packed_bytes(int out, int in) {
   return (size_t)q4k_tiles(out) * (size_t)q8_groups(in) * kQ8Record;

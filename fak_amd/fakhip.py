@@ -73,6 +73,9 @@ SIGNATURES = {
     "fhip_q4k_matmul_group_f32": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i]),
     "fhip_q4k_matmul_int8_f32": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "fhip_q6k_bytes": (C.c_size_t, [_i, _i]),
+    "fhip_q6k_packed_bytes": (C.c_size_t, [_i, _i]),
+    "fhip_q6k_repack": (_i, [_vp, _vp, _i, _i]),
+    "fhip_q6k_unpack": (_i, [_vp, _vp, _i, _i]),
     "fhip_q6k_upload": (_vp, [_vp, _i, _i]),
     "fhip_q6k_dequant_f32": (_i, [_vp, _vp, _i, _i]),
     "fhip_q6k_matmul_f32": (_i, [_vp, _vp, _vp, _i, _i, _i]),

@@ -23,7 +23,7 @@ def main() -> None:
     ap.add_argument("--m", type=int, default=1, help="tokens")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--q8", action="store_true", help="Q8_0 weights instead of Q4_K")
-    ap.add_argument("--q6k", action="store_true", help="raw Q6_K weights instead of Q4_K")
+    ap.add_argument("--q6k", action="store_true", help="Q6_K weights instead of Q4_K")
     ap.add_argument("--seed", type=int, default=1)
     a = ap.parse_args()
     fakhip.init()
@@ -35,8 +35,8 @@ def main() -> None:
         raw[:, 208:210] = (np.abs(rng.standard_normal(raw.shape[0])) * 1e-3).astype(
             np.float16).view(np.uint8).reshape(-1, 2)
         raw = raw.reshape(-1)
-        up, mm, nbytes = "fhip_q6k_upload", "fhip_q6k_matmul_f32", lib.fhip_q6k_bytes(a.n, a.k)
-        alg = nbytes
+        up, mm, nbytes = "fhip_q6k_upload", "fhip_q6k_matmul_f32", lib.fhip_q6k_packed_bytes(a.n, a.k)
+        alg = lib.fhip_q6k_bytes(a.n, a.k)
     elif a.q8:
         raw = synth.q8_0_weights(a.n, a.k, a.seed)
         up, mm, nbytes = "fhip_q8_0_upload", "fhip_q8_0_matmul_f32", lib.fhip_q8_0_packed_bytes(a.n, a.k)

@@ -136,16 +136,24 @@ int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, float *dY, in
 
 /* Bytes of a raw Q6_K weight [out][in] (in a multiple of 256); 0 for a bad shape. */
 size_t fhip_q6k_bytes(int out, int in);
-/* Copy raw GGUF Q6_K bytes to the device (kept in GGUF order): the resident-weight upload of
- * quantizeKQuantFromRaw(kind Q6_K) (internal/model/quant_kquant.go:236-250). */
+/* Bytes of the tiled device layout (16-row tiles of 3360-byte records; out padded to 16). */
+size_t fhip_q6k_packed_bytes(int out, int in);
+/* Device raw GGUF rows -> tiled layout, and back (lossless byte permutation). */
+int fhip_q6k_repack(void *dPacked, const uint8_t *dRaw, int out, int in);
+int fhip_q6k_unpack(uint8_t *dRaw, const void *dPacked, int out, int in);
+/* Allocate a tiled Q6_K weight and fill it from host raw GGUF bytes: the resident-weight upload
+ * of quantizeKQuantFromRaw(kind Q6_K) (internal/model/quant_kquant.go:236-250). Free with
+ * fhip_free. */
 void *fhip_q6k_upload(const uint8_t *hRaw, int out, int in);
-/* dW[out][in] = the dequantized weights, bit-identical to q6kDequantSuperBlock
- * (internal/model/quant_kquant.go:139-163). Test hook. */
-int fhip_q6k_dequant_f32(float *dW, const void *dRaw, int out, int in);
-/* Y[P][out] = X[P][in] @ W^T for a resident Q6_K weight: the replacement for
+/* dW[out][in] = the dequantized weights of a tiled Q6_K weight, bit-identical to
+ * q6kDequantSuperBlock (internal/model/quant_kquant.go:139-163). Test hook. */
+int fhip_q6k_dequant_f32(float *dW, const void *dPacked, int out, int in);
+/* Y[P][out] = X[P][in] @ W^T for a tiled Q6_K weight: the replacement for
  * kQuantMatRowsInto(kind Q6_K) (internal/model/quant_kquant.go:188-232), whose f32 route
- * dequantizes each super-block and dots it; bound max|dY|/RMS(Y) <= 1e-3. */
-int fhip_q6k_matmul_f32(const void *dRaw, const float *dX, float *dY, int out, int in, int P);
+ * dequantizes each super-block and dots it; bound max|dY|/RMS(Y) <= 1e-3. dX and the weight
+ * 16-byte aligned. */
+int fhip_q6k_matmul_f32(const void *dPacked, const float *dX, float *dY, int out, int in,
+                        int P);
 
 /* ---- Fused decode MLP (dense SwiGLU FFN of one decode step) ------------------------------- */
 

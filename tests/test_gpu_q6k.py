@@ -60,7 +60,8 @@ def test_gemv_reference_fixture_exact(hip, oracle_mod):
 
 
 @pytest.mark.parametrize("out,in_,P", [(1536, 3584, 1), (3584, 18944, 1), (152, 4096, 5),
-                                       (4096, 512, 3), (37, 256, 8)])
+                                       (4096, 512, 3), (37, 256, 8), (17, 66048, 1),
+                                       (152064, 3584, 1)])
 def test_gemv_matches_oracle(hip, oracle_mod, out, in_, P):
     print(f"[case] q6k gemv out={out} in={in_} P={P}", flush=True)
     rng = np.random.default_rng(out + in_ + P)
@@ -71,6 +72,27 @@ def test_gemv_matches_oracle(hip, oracle_mod, out, in_, P):
     err = rel_err(Y, ref)
     print(f"    max|d|/RMS = {err:.2e}", flush=True)
     assert err <= 1e-3
+
+
+@pytest.mark.parametrize("out,in_", [(1, 256), (16, 512), (37, 768), (300, 1024)])
+def test_repack_round_trip(hip, out, in_):
+    """The tiled layout is a byte permutation: repack then unpack returns the raw rows, and
+    the padding rows of the last tile are zero."""
+    lib = fakhip.load()
+    rng = np.random.default_rng(out + in_)
+    raw = rng.integers(0, 256, size=out * (in_ // 256) * 210, dtype=np.uint8)
+    nb = lib.fhip_q6k_packed_bytes(out, in_)
+    assert nb == -(-out // 16) * (in_ // 256) * 3360
+    with Dev.from_host(raw) as dr, Dev(nb) as dp, Dev(raw.nbytes) as back:
+        fakhip.call("fhip_q6k_repack", dp.ptr, dr.ptr, out, in_)
+        fakhip.call("fhip_q6k_unpack", back.ptr, dp.ptr, out, in_)
+        np.testing.assert_array_equal(back.to_host(np.uint8), raw)
+        packed = dp.to_host(np.uint8).reshape(-1, in_ // 256, 3360)
+        if out % 16:
+            tail = packed[-1]  # every record of the last tile: rows out%16.. are zero
+            r0 = out % 16
+            assert not tail[:, 16 * r0:256].any()        # scales
+            assert not tail[:, 256 + 2 * r0:288].any()   # d
 
 
 def test_argument_errors(hip):
