@@ -27,6 +27,7 @@ import ctypes as C
 import dataclasses
 import enum
 import os
+import weakref
 from typing import Optional
 
 import numpy as np
@@ -100,10 +101,9 @@ class HostBuf:
 class DevBuf:
     """A device-resident buffer: pointer into the fakhip pool + byte length."""
 
-    def __init__(self, ptr: int, nbytes: int, host_key=None):
+    def __init__(self, ptr: int, nbytes: int):
         self.ptr = ptr
         self.nbytes = nbytes
-        self.host_key = host_key
 
     def Ready(self) -> bool:
         return True
@@ -169,11 +169,10 @@ def NewQ8_0GGUF(be, shape, raw) -> Tensor:
 class DevQ8Buf:
     """A device HAL Q8 weight: codes and scales buffers from the fakhip pool."""
 
-    def __init__(self, codes: int, scales: int, block: int, host_key=None):
+    def __init__(self, codes: int, scales: int, block: int):
         self.ptr = codes
         self.scales = scales
         self.block = block
-        self.host_key = host_key
 
     def Ready(self) -> bool:
         return True
@@ -187,7 +186,9 @@ class RocmBackend:
 
     def __init__(self, kq_int8: Optional[bool] = None):
         self.info = fakhip.init()
-        self._upload_cache: dict = {}
+        # upload cache (cuda.go:680-704): (host address, weakref to the owning array, dtype,
+        # resident tensor)
+        self._upload_cache: list = []
         # The int8 Q4_K route is opt-in exactly as on the CPU: FAK_KQ_INT8 = 1 / on / true
         # (q4kInt8Default, internal/model/quant_amd64_q4k.go:54-61), resolved once here.
         if kq_int8 is None:
@@ -206,6 +207,32 @@ class RocmBackend:
 
     def Caps(self) -> Caps:
         return Caps(Async=True, UploadDtype=True, DeviceMemory=True, CapacityProbe=True)
+
+    @staticmethod
+    def _host_array(t: Tensor) -> np.ndarray:
+        return t.buf.i8 if t.buf.i8 is not None else t.buf.f32
+
+    @staticmethod
+    def _owner(a: np.ndarray) -> np.ndarray:
+        while isinstance(a.base, np.ndarray):
+            a = a.base
+        return a
+
+    def _cached(self, t: Tensor, dtype: Dtype):
+        """The reference shares one resident copy per host buffer address, dtype and element count
+        (cuda.go:680-692) and accepts that a freed buffer's address can be reused; here a hit also
+        needs the array that owns the memory to be alive, so a reused address never hits."""
+        a = self._host_array(t)
+        for ptr, owner, dt, res in self._upload_cache:
+            if ptr == a.ctypes.data and owner() is self._owner(a) and dt == dtype and \
+                    res.Numel() == t.Numel():
+                return res
+        return None
+
+    def _remember(self, t: Tensor, dtype: Dtype, res: Tensor) -> None:
+        a = self._host_array(t)
+        self._upload_cache = [e for e in self._upload_cache if e[1]() is not None]
+        self._upload_cache.append((a.ctypes.data, weakref.ref(self._owner(a)), dtype, res))
 
     # ---- residency ----
     def Upload(self, t: Tensor, as_: Dtype = Dtype.F32) -> Tensor:
@@ -239,18 +266,17 @@ class RocmBackend:
         if block <= 0 or in_ % block or codes.size != out * in_ or scale.size != out * (in_ // block):
             raise ValueError(f"compute: Q8_0 weight [{out},{in_}] block {block} has {codes.size} "
                              f"codes / {scale.size} scales")
-        key = (codes.ctypes.data, int(t.Dtype))
-        cached = self._upload_cache.get(key)
-        if cached is not None and cached.Numel() == t.Numel():
+        cached = self._cached(t, Dtype.Q8_0)
+        if cached is not None:
             return cached
         cp = fakhip.alloc_call("fhip_malloc", max(codes.size, 4))
         sp = fakhip.alloc_call("fhip_malloc", max(scale.size * 4, 4))
         if codes.size:
             fakhip.call("fhip_h2d", cp, codes.ctypes.data, codes.size)
             fakhip.call("fhip_h2d", sp, scale.ctypes.data, scale.size * 4)
-        res = Tensor(Dtype.Q8_0, Layout.RowMajor, [out, in_], t.Quant, DevQ8Buf(cp, sp, block, key),
+        res = Tensor(Dtype.Q8_0, Layout.RowMajor, [out, in_], t.Quant, DevQ8Buf(cp, sp, block),
                      self)
-        self._upload_cache[key] = res
+        self._remember(t, Dtype.Q8_0, res)
         return res
 
     def _narrow_q8(self, t: Tensor) -> Tensor:
@@ -265,9 +291,8 @@ class RocmBackend:
         f = t.buf.f32
         if f.size != out * in_:
             raise ValueError(f"compute: f32 weight has {f.size} elements, want {out}x{in_}")
-        key = (f.ctypes.data, int(Dtype.Q8_0))
-        cached = self._upload_cache.get(key)
-        if cached is not None and cached.Numel() == t.Numel():
+        cached = self._cached(t, Dtype.Q8_0)
+        if cached is not None:
             return cached
         nblk = in_ // blk
         cp = fakhip.alloc_call("fhip_malloc", max(out * in_, 4))
@@ -282,8 +307,8 @@ class RocmBackend:
                 fakhip.load().fhip_free(tmp)
         res = Tensor(Dtype.Q8_0, Layout.RowMajor, [out, in_],
                      QuantSpec(Block=blk, Axis=2, Bits=8, Symmetric=True),
-                     DevQ8Buf(cp, sp, blk, key), self)
-        self._upload_cache[key] = res
+                     DevQ8Buf(cp, sp, blk), self)
+        self._remember(t, Dtype.Q8_0, res)
         return res
 
     def _upload_quant(self, t: Tensor, fn: str, block: int, block_bytes: int) -> Tensor:
@@ -296,13 +321,12 @@ class RocmBackend:
         want = out * (in_ // block) * block_bytes
         if raw.size != want:
             raise ValueError(f"compute: {t.Dtype} payload size {raw.size} != {want}")
-        key = (raw.ctypes.data, int(t.Dtype))
-        cached = self._upload_cache.get(key)
-        if cached is not None and cached.Numel() == t.Numel():
+        cached = self._cached(t, t.Dtype)
+        if cached is not None:
             return cached
         ptr = fakhip.alloc_call(fn, raw.ctypes.data, out, in_)
-        res = Tensor(t.Dtype, Layout.Tiled, [out, in_], t.Quant, DevBuf(ptr, want, key), self)
-        self._upload_cache[key] = res
+        res = Tensor(t.Dtype, Layout.Tiled, [out, in_], t.Quant, DevBuf(ptr, want), self)
+        self._remember(t, t.Dtype, res)
         return res
 
     def Host(self, t: Tensor):
@@ -319,8 +343,7 @@ class RocmBackend:
 
     def Free(self, t: Tensor) -> None:
         if isinstance(t.buf, (DevBuf, DevQ8Buf)) and t.buf.ptr:
-            if t.buf.host_key is not None:
-                self._upload_cache.pop(t.buf.host_key, None)
+            self._upload_cache = [e for e in self._upload_cache if e[3].buf is not t.buf]
             fakhip.load().fhip_free(t.buf.ptr)
             t.buf.ptr = 0
             if isinstance(t.buf, DevQ8Buf) and t.buf.scales:

@@ -78,6 +78,27 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
+HOST = os.path.join(HERE, "host")
+HOST_LIB = os.path.join(HERE, "libfakhost.so")
+HOST_CXXFLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-I", os.path.join(ROOT, "include")]
+
+
+def build_host(verbose: bool = False) -> str:
+    """The C++ host side (fak_amd/host: the compute.Backend seam over the C ABI) ->
+    fak_amd/libfakhost.so, linked against libfakhip.so (found next to it at run time)."""
+    srcs = sorted(glob.glob(os.path.join(HOST, "*.cpp")))
+    tmp = HOST_LIB + ".tmp%d" % os.getpid()
+    cmd = ["g++", *HOST_CXXFLAGS, "-shared", *srcs, "-L", HERE, "-lfakhip",
+           "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed for the host library:\n{r.stdout}{r.stderr}")
+    os.replace(tmp, HOST_LIB)
+    return HOST_LIB
+
+
 def build(verbose: bool = False, jobs: int = 8) -> str:
     os.makedirs(BUILD, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
@@ -89,6 +110,7 @@ def build(verbose: bool = False, jobs: int = 8) -> str:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
+    build_host(verbose)
     return LIB
 
 

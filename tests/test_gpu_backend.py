@@ -106,3 +106,22 @@ def test_shape_errors_raise(be):
     with pytest.raises(NotImplementedError):
         be.RMSNorm(None, None, 1e-6)
     be.Free(wq)
+
+
+def test_upload_cache_never_stale(be, oracle_mod):
+    """A host tensor that is gone (its memory free for reuse by the next one) never hits the
+    upload cache: every round's weight is its own."""
+    out, in_ = 16, 256
+    x = synth.activations(1, in_, 3)[0]
+    xd = be.Upload(B.NewF32(be, [in_], x), B.Dtype.F32)
+    kept = []
+    for r in range(4):
+        raw = synth.q4k_weights(out, in_, 100 + r)
+        w = be.Upload(B.NewQ4K(be, [out, in_], raw.copy()), B.Dtype.Q4_K)  # host tensor dies
+        y = be.Read(be.MatMul(w, xd))
+        ref = oracle_mod.q4k_matrows(raw, out, in_, x)
+        assert rel_err(y, ref) <= 1e-3, r
+        kept.append(w)
+    for w in kept:
+        be.Free(w)
+    be.Free(xd)
