@@ -39,7 +39,7 @@ RESOURCE_REMARK = "kernel-resource-usage"
 # Kernels allowed a small, measured spill (mangled-name fragment -> bytes per lane): the
 # three-workgroups-per-CU prefill GEMM keeps one 16-byte staging value in scratch once per
 # super-block (measured faster than the spill-free two-workgroup form: 116 vs 131 us at M=512).
-SCRATCH_ALLOWED = {"q4k_gemm32_kernelILi1ELi3E": 32}
+SCRATCH_ALLOWED = {"quant_gemm32_kernelILi0ELi1ELi3E": 32}
 
 
 def scratch_kernels(remarks: str) -> list[tuple[str, int]]:

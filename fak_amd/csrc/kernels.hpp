@@ -48,6 +48,8 @@ int q4k_gemv_ws(const void *W, const float *X, float *Y, int N, int K, int M, vo
 int q6k_gemv(const void *W, const float *X, float *Y, int N, int K, int M);
 int q4k_gemm(const void *W, const float *X, float *Y, int N, int K, int M);
 int q4k_gemm32(const void *W, const float *X, float *Y, int N, int K, int M);
+// The same GEMM over a tiled Q6_K weight (prefill of the q4_k_m Q6_K tensors).
+int q6k_gemm32(const void *W, const float *X, float *Y, int N, int K, int M);
 int q8_0_gemv(const void *W, const float *X, float *Y, int N, int K, int M);
 
 // __builtin_amdgcn_sched_barrier mask: every instruction class except vector-memory ones may be

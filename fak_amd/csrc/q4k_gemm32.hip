@@ -16,6 +16,12 @@
 // The MFMA sums over K, so any mapping of (lane group, element) to K positions works as long
 // as both operands use it: here the K16 slice q holds positions 16q + 8 (lane / 32) + perm8(j),
 // which is where the nibble unpack leaves the weights.
+//
+// The same kernel runs Q6_K weights (FMT 1) from the Q6_K tiled records (tiled.hpp): the K16
+// slice q of a row is its 16-weight group q, whose codes sit in one 16-byte ql unit (a nibble)
+// and one 16-byte qh unit (a 2-bit field); a lane takes the 8 codes of its half (8 kap ..) and
+// makes w = (c - 32) * f16(d * sc) in f16: (1024 + c) - 1056 is exact, one rounding for the
+// product.
 #include "kernels.hpp"
 
 namespace fhip {
@@ -87,12 +93,43 @@ __device__ __forceinline__ void dequant8(uint32_t x0, uint32_t x1, const RowScal
   bh = __builtin_bit_cast(f16x8, hh);
 }
 
+// Q6_K: the 8 codes of slices a (group g' = h) and b (g' = 2 + h) of chunk c = 2 h' + k from
+// their ql bytes (nibble k) and the shared qh bytes (fields 4k and 4k + 2), as f16 weights.
+__device__ __forceinline__ void dequant6(uint2 qa, uint2 qb, uint2 qh, int k, _Float16 Sa,
+                                         _Float16 Sb, uint32_t m0F, uint32_t m03,
+                                         const Magic &K, f16x8 &ba, f16x8 &bb) {
+  const h2 k1056 = {(_Float16)1056.f, (_Float16)1056.f};
+  const h2 SA = {Sa, Sa}, SB = {Sb, Sb};
+  const uint32_t qav[2] = {qa.x, qa.y}, qbv[2] = {qb.x, qb.y}, qhv[2] = {qh.x, qh.y};
+  u32x4 ra, rb;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const uint32_t ca = ((qav[m] >> (4 * k)) & m0F) | (((qhv[m] >> (4 * k)) & m03) << 4);
+    const uint32_t cb = ((qbv[m] >> (4 * k)) & m0F) | (((qhv[m] >> (4 * k + 2)) & m03) << 4);
+    // bytes (0, 2) and (1, 3) of each code word: elements in perm8 order
+    ra[2 * m] = as_u((as_h2((ca & K.byte02) | K.magic) - k1056) * SA);
+    ra[2 * m + 1] = as_u((as_h2(((ca >> 8) & K.byte02) | K.magic) - k1056) * SA);
+    rb[2 * m] = as_u((as_h2((cb & K.byte02) | K.magic) - k1056) * SB);
+    rb[2 * m + 1] = as_u((as_h2(((cb >> 8) & K.byte02) | K.magic) - k1056) * SB);
+  }
+  ba = __builtin_bit_cast(f16x8, ra);
+  bb = __builtin_bit_cast(f16x8, rb);
+}
+
 constexpr int kBM = 128;               // tokens per workgroup
 constexpr int kBT = 8;                 // 16-row tiles per workgroup (128 rows)
 constexpr int kAU = 4 * 4 * 64;        // uint4 units of one activation stage (4 tiles x 4 K16)
-constexpr int kWU = kBT * kQ4kRecord / 16;  // uint4 units of one super-block's records (1152)
-constexpr int kWPT = (kWU + 255) / 256;     // per thread (5); the last 128 threads' fifth unit
-constexpr int kWUP = kWPT * 256;            // re-reads a valid unit into LDS padding
+
+// Per weight format: record bytes, uint4 units of one super-block's records for the workgroup's
+// 8 row tiles, units per thread (the last threads re-read a valid unit into LDS padding).
+template <int FMT>
+struct GemmFmt {
+  static constexpr int kRec = FMT == 0 ? kQ4kRecord : kQ6kRecord;
+  static constexpr int kUnits = kRec / 16;         // 144 or 210
+  static constexpr int kWU = kBT * kUnits;         // 1152 or 1680
+  static constexpr int kWPT = (kWU + 255) / 256;   // 5 or 7
+  static constexpr int kWUP = kWPT * 256;
+};
 
 // Activation operands: xa[(tt * (K/16) + q) * 64 + l] = 8 f16 of token 32 tt + l % 32 at
 // K = 16 q + 8 (l / 32) + perm8(j); token tiles padded to whole workgroups (zeros).
@@ -120,13 +157,16 @@ __global__ void gemm32_xprep_kernel(const float *__restrict__ X, int M, int K, l
   xa[id] = __builtin_bit_cast(uint4, h);
 }
 
-// NWB: LDS buffers for the weight records (2: the next super-block loads while the current one
-// is read; 1: a second barrier per super-block, 52 KB of LDS, three workgroups per CU).
-template <int NWB, int WPE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void q4k_gemm32_kernel(const uint8_t *__restrict__ W,
+// FMT: 0 Q4_K, 1 Q6_K. NWB: LDS buffers for the weight records (2: the next super-block loads
+// while the current one is read; 1: a second barrier per super-block; Q4_K with one buffer uses
+// 52 KB of LDS, three workgroups per CU).
+template <int FMT, int NWB, int WPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void quant_gemm32_kernel(const uint8_t *__restrict__ W,
                                                          const uint4 *__restrict__ xa,
                                                          float *__restrict__ Y, int N, int M,
                                                          int nblk, int ntiles, int MTG) {
+  using F = GemmFmt<FMT>;
+  constexpr int kRec = F::kRec, kWU = F::kWU, kWPT = F::kWPT, kWUP = F::kWUP;
   __shared__ u32x4 As[2][kAU];
   __shared__ u32x4 Ws[NWB][kWUP];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -145,28 +185,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   // 16-byte unit offsets from xg / W (32-bit). Unit tid + 256 k of an activation stage is token
   // tile k, K16 slice tid >> 6, lane tid & 63: a uniform stride of one token tile per k.
   const uint32_t aoff = (uint32_t)(tid >> 6) * 64 + lane, astride = (uint32_t)nq * 64;
-  // Weight unit tid + 256 k is record rec_k = u / 144, unit off_k = u % 144 of it (u past the
-  // 1152 real units re-reads unit 0); the five (rec, off) pairs are packed 12 bits each.
+  // Weight unit tid + 256 k is record rec_k = u / units, unit off_k = u % units of it (u past
+  // the real units re-reads unit 0). Q4_K packs the five (rec, off) pairs 12 bits each.
   uint64_t wpack = 0;
+  if (FMT == 0) {
 #pragma unroll
-  for (int k = 0; k < kWPT; ++k) {
-    const int u = tid + 256 * k < kWU ? tid + 256 * k : 0;
-    const int rec = u / (kQ4kRecord / 16), off = u - rec * (kQ4kRecord / 16);
-    wpack |= (uint64_t)((rec << 8) | off) << (12 * k);
+    for (int k = 0; k < kWPT; ++k) {
+      const int u = tid + 256 * k < kWU ? tid + 256 * k : 0;
+      const int rec = u / F::kUnits, off = u - rec * F::kUnits;
+      wpack |= (uint64_t)((rec << 8) | off) << (12 * k);
+    }
   }
   const int tile0 = kBT * ng;
   auto woff = [&](int k) {
-    uint64_t wp = wpack;
-    asm volatile("" : "+v"(wp));  // recomputed per load, not hoisted into five live registers
-    const uint32_t f = (uint32_t)(wp >> (12 * k)) & 0xFFFu;
-    const int T = min(tile0 + (int)(f >> 8), ntiles - 1);
-    return (uint32_t)T * nblk * (kQ4kRecord / 16) + (f & 0xFFu);
+    uint32_t rec, off;
+    if (FMT == 0) {
+      uint64_t wp = wpack;
+      asm volatile("" : "+v"(wp));  // recomputed per load, not hoisted into five live registers
+      const uint32_t f = (uint32_t)(wp >> (12 * k)) & 0xFFFu;
+      rec = f >> 8;
+      off = f & 0xFFu;
+    } else {
+      const int u = tid + 256 * k < kWU ? tid + 256 * k : 0;
+      rec = (uint32_t)(u / F::kUnits);
+      off = (uint32_t)u - rec * F::kUnits;
+    }
+    const int T = min(tile0 + (int)rec, ntiles - 1);
+    return (uint32_t)T * nblk * F::kUnits + off;
   };
   const u32x4 *Wv = reinterpret_cast<const u32x4 *>(W);
 #define LOAD_A(st, regs)                                                             \
   _Pragma("unroll") for (int k = 0; k < 4; ++k) regs[k] = xg[aoff + k * astride + (uint32_t)(st) * 256];
 #define LOAD_W(b, regs)                                                              \
-  _Pragma("unroll") for (int k = 0; k < kWPT; ++k) regs[k] = Wv[woff(k) + (uint32_t)(b) * (kQ4kRecord / 16)];
+  _Pragma("unroll") for (int k = 0; k < kWPT; ++k) regs[k] = Wv[woff(k) + (uint32_t)(b) * F::kUnits];
 #define STORE_W(buf, regs) \
   _Pragma("unroll") for (int k = 0; k < kWPT; ++k) Ws[buf][tid + 256 * k] = regs[k];
 
@@ -195,8 +246,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     const int wb = NWB == 2 ? (b & 1) : 0;
     const unsigned char *wbase = reinterpret_cast<const unsigned char *>(Ws[wb]);
     RowScales rs[2];
-    rs[0] = row_scales(__builtin_bit_cast(uint4, *reinterpret_cast<const u32x4 *>(wbase + Tl0 * kQ4kRecord + 16 * r16)), K);
-    rs[1] = row_scales(__builtin_bit_cast(uint4, *reinterpret_cast<const u32x4 *>(wbase + Tl1 * kQ4kRecord + 16 * r16)), K);
+    uint4 sc6[2];  // Q6_K: the row's 16 int8 scales
+    float d6[2];   // Q6_K: the row's d
+    if (FMT == 0) {
+      rs[0] = row_scales(__builtin_bit_cast(uint4, *reinterpret_cast<const u32x4 *>(wbase + Tl0 * kRec + 16 * r16)), K);
+      rs[1] = row_scales(__builtin_bit_cast(uint4, *reinterpret_cast<const u32x4 *>(wbase + Tl1 * kRec + 16 * r16)), K);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const unsigned char *rec = wbase + (t ? Tl1 : Tl0) * kRec;
+        sc6[t] = __builtin_bit_cast(uint4, *reinterpret_cast<const u32x4 *>(rec + 16 * r16));
+        d6[t] = (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t *>(rec + kQ6kD + 2 * r16));
+      }
+    }
     const bool more = b + 1 < nblk;
     if (more) {
       LOAD_W(b + 1, wreg)
@@ -207,22 +269,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
       if (st + 1 < nst) {
         LOAD_A(st + 1, areg)
       }
-      // nibble bytes: lane group g = 2h + kap of chunk c, for both MFMA row tiles
-      uint2 xb[2][2];
+      // Q4_K: nibble bytes of lane group g = 2h + kap of chunk c, for both MFMA row tiles.
+      // Q6_K: ql bytes of groups 4c + h and 4c + 2 + h and their qh bytes (half kap).
+      uint2 xb[2][2], x6[2][2][3];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int T = t ? Tl1 : Tl0, g = 2 * h + kap;
-          xb[t][h] = *reinterpret_cast<const uint2 *>(wbase + T * kQ4kRecord + kQ4kHdr +
-                                                      1024 * (c >> 1) + 16 * (16 * g + r16) +
-                                                      8 * (c & 1));
+          const int T = t ? Tl1 : Tl0;
+          if (FMT == 0) {
+            const int g = 2 * h + kap;
+            xb[t][h] = *reinterpret_cast<const uint2 *>(wbase + T * kRec + kQ4kHdr +
+                                                        1024 * (c >> 1) + 16 * (16 * g + r16) +
+                                                        8 * (c & 1));
+          } else {
+            const unsigned char *rec = wbase + T * kRec;
+            const int hh = c >> 1;
+            x6[t][h][0] = *reinterpret_cast<const uint2 *>(rec + kQ6kQl + 1024 * hh +
+                                                           16 * (16 * h + r16) + 8 * kap);
+            x6[t][h][1] = *reinterpret_cast<const uint2 *>(rec + kQ6kQl + 1024 * hh +
+                                                           16 * (16 * (2 + h) + r16) + 8 * kap);
+            x6[t][h][2] = *reinterpret_cast<const uint2 *>(rec + kQ6kQh + 512 * hh + 256 * h +
+                                                           16 * r16 + 8 * kap);
+          }
         }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         f16x8 bl[2], bh[2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) dequant8(xb[t][h].x, xb[t][h].y, rs[t], c, K, bl[t], bh[t]);
+        for (int t = 0; t < 2; ++t) {
+          if (FMT == 0) {
+            dequant8(xb[t][h].x, xb[t][h].y, rs[t], c, K, bl[t], bh[t]);
+          } else {
+            const uint32_t scw = c == 0 ? sc6[t].x : c == 1 ? sc6[t].y : c == 2 ? sc6[t].z : sc6[t].w;
+            const _Float16 Sa = (_Float16)(d6[t] * (float)(int8_t)(scw >> (8 * h)));
+            const _Float16 Sb = (_Float16)(d6[t] * (float)(int8_t)(scw >> (8 * (2 + h))));
+            dequant6(x6[t][h][0], x6[t][h][1], x6[t][h][2], c & 1, Sa, Sb,
+                     in_reg(0x0F0F0F0Fu), in_reg(0x03030303u), K, bl[t], bh[t]);
+          }
+        }
 #pragma unroll
         for (int hi = 0; hi < 2; ++hi) {
           const int ql = 2 * hi + h;  // K16 slice within the chunk
@@ -273,7 +358,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 
 size_t gemm32_xa_bytes(int M, int K) { return (size_t)ceil_div(M, kBM) * kBM * K * 2; }
 
-int q4k_gemm32(const void *Wv, const float *X, float *Y, int N, int K, int M) {
+namespace {
+int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int K, int M) {
   const int nblk = K / 256;
   uint4 *xa = (uint4 *)workspace(gemm32_xa_bytes(M, K));
   if (!xa) return FHIP_ENOMEM;
@@ -283,16 +369,28 @@ int q4k_gemm32(const void *Wv, const float *X, float *Y, int N, int K, int M) {
   FHIP_CHECK_LAUNCH("gemm32_xprep_kernel");
   const int ntiles = q4k_tiles(N);
   const int grid = MTG * ceil_div(ntiles, kBT);
-  int nwb = env_int("FAK_HIP_GEMM32_NWB");
-  if (nwb == 0) nwb = 1;
-  if (nwb == 1)
-    q4k_gemm32_kernel<1, 3><<<grid, 256, 0, stream()>>>((const uint8_t *)Wv, xa, Y, N, M, nblk,
-                                                        ntiles, MTG);
-  else
-    q4k_gemm32_kernel<2, 2><<<grid, 256, 0, stream()>>>((const uint8_t *)Wv, xa, Y, N, M, nblk,
-                                                        ntiles, MTG);
-  FHIP_CHECK_LAUNCH("q4k_gemm32_kernel");
+  const uint8_t *W = (const uint8_t *)Wv;
+  if (fmt == 1) {  // 60 KB of LDS with one weight buffer: two workgroups per CU
+    quant_gemm32_kernel<1, 1, 2><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
+  } else {
+    int nwb = env_int("FAK_HIP_GEMM32_NWB");
+    if (nwb == 0) nwb = 1;
+    if (nwb == 1)
+      quant_gemm32_kernel<0, 1, 3><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
+    else
+      quant_gemm32_kernel<0, 2, 2><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
+  }
+  FHIP_CHECK_LAUNCH("quant_gemm32_kernel");
   return FHIP_OK;
+}
+}  // namespace
+
+int q4k_gemm32(const void *Wv, const float *X, float *Y, int N, int K, int M) {
+  return launch_gemm32(0, Wv, X, Y, N, K, M);
+}
+
+int q6k_gemm32(const void *Wv, const float *X, float *Y, int N, int K, int M) {
+  return launch_gemm32(1, Wv, X, Y, N, K, M);
 }
 
 }  // namespace fhip

@@ -325,8 +325,10 @@ int launch_q6k_gemv(const uint8_t *W, const float *x, float *y, int N, int K) {
 
 }  // namespace
 
-// Q6_K GEMV over any number of tokens (one launch per token) on the tiled layout.
+// Q6_K matmul on the tiled layout: up to 16 tokens one GEMV launch per token (max|dY|/RMS
+// <= 1e-3), more through the f16 MFMA prefill GEMM (q4k_gemm32.hip, <= 1e-2).
 int q6k_gemv(const void *dW, const float *dX, float *dY, int out, int in, int P) {
+  if (P > 16) return q6k_gemm32(dW, dX, dY, out, in, P);
   for (int t = 0; t < P; ++t)
     if (int rc = launch_q6k_gemv((const uint8_t *)dW, dX + (size_t)t * in, dY + (size_t)t * out,
                                  out, in))
