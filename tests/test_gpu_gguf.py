@@ -81,3 +81,40 @@ def test_load_resident_selects_names(hip, tmp_path):
         finally:
             for w in res.values():
                 w.free()
+
+
+def test_q4_k_m_layer_fused_mlp(hip, oracle_mod, tmp_path):
+    """A q4_k_m-style FFN block (Q4_K ffn_gate / ffn_up [I, H], Q6_K ffn_down [H, I]) read from a
+    GGUF file, made resident straight from the mapped bytes and run through the fused decode MLP:
+    within the GEMV bound (max|dY|/RMS <= 1e-3) of the oracle's denseSwiGLU chain on the file's
+    own bytes, for one and three tokens."""
+    H, I = 512, 1536
+    rng = np.random.default_rng(23)
+    down = qc.pin_d(rng.integers(0, 256, H * (I // 256) * 210, dtype=np.uint8), 0x1000)
+    tens = [("blk.0.ffn_gate.weight", [H, I], TensorType.Q4_K, synth.q4k_weights(I, H, 41)),
+            ("blk.0.ffn_up.weight", [H, I], TensorType.Q4_K, synth.q4k_weights(I, H, 42)),
+            ("blk.0.ffn_down.weight", [I, H], TensorType.Q6_K, down)]
+    path = str(tmp_path / "layer.gguf")
+    gguf.write(path, [("general.architecture", gguf.ValueType.STRING, "qwen2")],
+               [(n, d, t, np.asarray(r, np.uint8).tobytes()) for n, d, t, r in tens])
+    with gguf.WeightSource(path) as ws:
+        res = gguf.load_resident(ws)
+        try:
+            g, u, d = (res[f"blk.0.ffn_{k}.weight"] for k in ("gate", "up", "down"))
+            assert g.shape == [I, H] and u.shape == [I, H] and d.shape == [H, I]
+            assert d.type == TensorType.Q6_K
+            raw = {k: np.frombuffer(ws.tensor_bytes(f"blk.0.ffn_{k}.weight"), np.uint8).copy()
+                   for k in ("gate", "up", "down")}
+            for P in (1, 3):
+                print(f"[gguf] q4_k_m FFN H={H} I={I} P={P}", flush=True)
+                X = synth.activations(P, H, 60 + P)
+                with Dev.from_host(X) as dx, Dev(P * H * 4) as dy:
+                    hip.call("fhip_q4k_mlp_q6down_f32", g.ptr, u.ptr, d.ptr, dx.ptr, dy.ptr, H, I, P)
+                    Y = dy.to_host(np.float32).reshape(P, H)
+                ref = oracle_mod.q4k_mlp(raw["gate"], raw["up"], raw["down"], H, I, X, P,
+                                         down_q6=True, workers=8)
+                assert np.all(np.isfinite(Y))
+                assert rel_err(Y, ref) <= 1e-3, (P, rel_err(Y, ref))
+        finally:
+            for w in res.values():
+                w.free()

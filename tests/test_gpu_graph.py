@@ -92,3 +92,71 @@ def test_graph_replays_match_eager(hip):
 def test_graph_begin_needs_a_created_stream(hip):
     fakhip.call("fhip_set_stream", None)
     assert fakhip.load().fhip_graph_begin() == -1
+
+
+def test_graph_decode_ffn_replays(hip):
+    """A decode step's FFN captured once: the fused MLP (Q4_K down and the q4_k_m Q6_K down, one
+    and three tokens) and Q6_K matmuls (GEMV and prefill GEMM) replay to the bits of the same
+    calls run eagerly, replay after replay, with new activations between replays."""
+    print("[case] graph capture: fused MLP (q4/q6 down), q6k gemv/gemm", flush=True)
+    from tests import q6k_cases as qc
+    lib = fakhip.load()
+    st = C.c_void_p()
+    fakhip.call("fhip_stream_create", C.byref(st))
+    fakhip.call("fhip_set_stream", st)
+    allocs, devs = [], []
+    try:
+        H, I = 512, 1024
+        rng = np.random.default_rng(5)
+        q6raw = qc.pin_d(rng.integers(0, 256, H * (I // 256) * 210, dtype=np.uint8), 0x1000)
+        g = fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(I, H, 31).ctypes.data, I, H)
+        u = fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(I, H, 32).ctypes.data, I, H)
+        d4 = fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(H, I, 33).ctypes.data, H, I)
+        d6 = fakhip.alloc_call("fhip_q6k_upload", q6raw.ctypes.data, H, I)
+        allocs += [g, u, d4, d6]
+        x3 = Dev(3 * H * 4)
+        xi = Dev(20 * I * 4)
+        devs += [x3, xi]
+        names = [("mlp1", H), ("mlp3", 3 * H), ("mlp6", 3 * H), ("q6gemv", H), ("q6gemm", 20 * H)]
+        outs = {nm: (Dev(n * 4), Dev(n * 4)) for nm, n in names}
+        for a, b in outs.values():
+            devs += [a, b]
+
+        def run(k):
+            fakhip.call("fhip_q4k_mlp_f32", g, u, d4, x3.ptr, outs["mlp1"][k].ptr, H, I, 1)
+            fakhip.call("fhip_q4k_mlp_f32", g, u, d4, x3.ptr, outs["mlp3"][k].ptr, H, I, 3)
+            fakhip.call("fhip_q4k_mlp_q6down_f32", g, u, d6, x3.ptr, outs["mlp6"][k].ptr, H, I, 3)
+            fakhip.call("fhip_q6k_matmul_f32", d6, xi.ptr, outs["q6gemv"][k].ptr, H, I, 1)
+            fakhip.call("fhip_q6k_matmul_f32", d6, xi.ptr, outs["q6gemm"][k].ptr, H, I, 20)
+
+        def set_x(seed):
+            fakhip.call("fhip_h2d", x3.ptr, synth.activations(3, H, seed).ctypes.data, 3 * H * 4)
+            fakhip.call("fhip_h2d", xi.ptr, synth.activations(20, I, seed + 1).ctypes.data,
+                        20 * I * 4)
+
+        set_x(300)
+        run(0)  # eager warm-up: sizes the workspace before capture
+        fakhip.call("fhip_sync")
+        fakhip.call("fhip_graph_begin")
+        run(0)
+        graph = C.c_void_p()
+        fakhip.call("fhip_graph_end", C.byref(graph))
+        try:
+            for rep in range(3):
+                set_x(400 + 10 * rep)
+                run(1)
+                fakhip.call("fhip_graph_launch", graph)
+                fakhip.call("fhip_stream_sync", st)
+                for nm, _ in names:
+                    a, b = outs[nm]
+                    assert np.array_equal(a.to_host(np.uint32), b.to_host(np.uint32)), (rep, nm)
+                print(f"    replay {rep}: all {len(names)} outputs bit-identical", flush=True)
+        finally:
+            fakhip.call("fhip_graph_destroy", graph)
+    finally:
+        fakhip.call("fhip_set_stream", None)
+        for d in devs:
+            d.close()
+        for p in allocs:
+            lib.fhip_free(p)
+        fakhip.call("fhip_stream_destroy", st)
