@@ -101,6 +101,34 @@ def test_q4k_gemm_prefill_7b(hip, oracle_mod, P):
     _check_q4k(oracle_mod, 18944, 3584, P, seed=512 + P, tol=GEMM_TOL, rows=256)
 
 
+@pytest.mark.parametrize("out,in_,P", [(300, 768, 600), (1000, 2048, 520), (64, 256, 1000),
+                                       (18944, 3584, 512)])
+def test_q4k_gemm_forms_bit_identical(hip, oracle_mod, monkeypatch, out, in_, P):
+    """The staged two-wave GEMM (the default above 384 tokens) and the four-wave GEMM share the
+    tile, the K order and each accumulator's MFMA sequence: their outputs agree bit for bit, on
+    whole and ragged row / token tiles, and the staged result meets the GEMM bound against the
+    oracle (sampled rows at the 7B shape)."""
+    print(f"[case] gemm forms out={out} in={in_} P={P}", flush=True)
+    raw = synth.q4k_weights(out, in_, seed=out + 3 * P)
+    X = synth.activations(P, in_, seed=P + 5)
+    monkeypatch.setenv("FAK_HIP_GEMM32_FORM", "1")
+    Y1 = q4k_matmul(raw, out, in_, X, P)
+    monkeypatch.setenv("FAK_HIP_GEMM32_FORM", "2")
+    Y2 = q4k_matmul(raw, out, in_, X, P)
+    monkeypatch.delenv("FAK_HIP_GEMM32_FORM")
+    assert np.array_equal(Y1.view(np.uint32), Y2.view(np.uint32))
+    if out > 4096:
+        rb = (in_ // 256) * 144
+        sel = np.concatenate([np.arange(0, 128), np.arange(out - 128, out)])
+        sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
+        ref = oracle_mod.q4k_gemm(sub, len(sel), in_, X, P, workers=16)
+        got = Y2[:, sel]
+    else:
+        ref = oracle_mod.q4k_gemm(raw, out, in_, X, P, workers=16)
+        got = Y2
+    assert rel_err(got, ref) <= GEMM_TOL
+
+
 def test_q4k_gemm_equals_gemv_per_token_within_tolerance(hip, oracle_mod):
     """The reference pins GEMM(o,t) == GEMV(X_t)(o) bitwise on the CPU; on the device the two
     kernels use different precisions, so each is held to its own bound against the same oracle
