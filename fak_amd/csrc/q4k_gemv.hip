@@ -1,5 +1,5 @@
 // q4k_gemv.hip — small-M (1..4 tokens) Q4_K matmul: the decode GEMV run for every generated
-// token, and narrow speculative-verify batches. Wider batches (5..16) use q4k_gemv_wide.hip.
+// token, and narrow speculative-verify batches. Wider batches (5..16) use q4k_gemv16.hip.
 //
 // Computes Y[t][o] = sum_k W[o][k] * X[t][k] with W the dequantized Q4_K weight
 // (w = d*sc_s*n - dmin*m_s for sub-block s, internal/model/quant_q4k.go:90-111) without ever
@@ -612,11 +612,13 @@ size_t gemv_i8_ws_bytes(int ntiles, int K, int M, bool swiglu) {
   return p.xop_bytes + p.part_bytes;
 }
 
-// Small-M entry: 1..4 tokens on the int8 kernel (FAK_HIP_GEMV_WIDE=1 forces the f16 one),
-// 5..16 on the f16 kernel of q4k_gemv_wide.hip.
+// Small-M entry: 1..4 tokens on the int8 kernel, 5..16 on the 32x32 MFMA kernel of
+// q4k_gemv16.hip (FAK_HIP_GEMV_WIDE=1 forces the older f16 kernel of q4k_gemv_wide.hip for
+// every width).
 int q4k_gemv(const void *Wv, const float *X, float *Y, int N, int K, int M) {
   if (M < 1 || M > 16) return fail(FHIP_EINVAL, "q4k_gemv: M=%d outside 1..16", M);
-  if (M > 4 || env_int("FAK_HIP_GEMV_WIDE")) return q4k_gemv_wide(Wv, X, Y, N, K, M);
+  if (env_int("FAK_HIP_GEMV_WIDE")) return q4k_gemv_wide(Wv, X, Y, N, K, M);
+  if (M > 4) return q4k_gemv16(Wv, X, Y, N, K, M);
   GemvGroup g = {};
   g.W[0] = (const uint8_t *)Wv;
   g.Y[0] = Y;
@@ -632,8 +634,11 @@ int q4k_gemv(const void *Wv, const float *X, float *Y, int N, int K, int M) {
 int q4k_gemv_group(const GemvGroup &g, const float *X, int K, int M) {
   if (M < 1 || M > 16) return fail(FHIP_EINVAL, "q4k_gemv_group: M=%d outside 1..16", M);
   if (M > 4 || env_int("FAK_HIP_GEMV_WIDE")) {
+    const bool wide = env_int("FAK_HIP_GEMV_WIDE") != 0;
     for (int i = 0; i < g.count; ++i)
-      if (int rc = q4k_gemv_wide(g.W[i], X, g.Y[i], g.N[i], K, M)) return rc;
+      if (int rc = wide ? q4k_gemv_wide(g.W[i], X, g.Y[i], g.N[i], K, M)
+                        : q4k_gemv16(g.W[i], X, g.Y[i], g.N[i], K, M))
+        return rc;
     return FHIP_OK;
   }
   return launch_i8_any(g, X, K, M);

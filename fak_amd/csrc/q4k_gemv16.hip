@@ -1,0 +1,348 @@
+// q4k_gemv16.hip — Q4_K matmul for 5..16 tokens (speculative verify) on the 32x32x16 f16 MFMA.
+//
+// Y[t][o] = sum_k W[o][k] X[t][k] with W the Q4_K weight (w = d*sc_s*n - dmin*m_s per 32-weight
+// sub-block s, internal/model/quant_q4k.go:90-111). Per super-block b of row o and token t
+//   sum_k w x = d * sum_s sc_s * (sum_{k in s} n_k x_k)  -  dmin * sum_s m_s * S_s,
+// S_s = sum_{k in s} x_k. Both sums run on the MFMA with exact operands:
+//   * weight operand: the integer sc_s * n_k (<= 63 * 15 = 945), exact in f16, made from a
+//     nibble pair with one and-or and one packed fma: (1024 + n) * sc - 1024 * sc, or for the
+//     high nibbles masked in place (1024 + 16 n) * (sc / 16) - 64 * sc. The fma rounds once and
+//     the result is an integer below 2048, so it is exact;
+//   * activation operand: 32 operand rows, the f16 of x (rows 0..15 = tokens 0..15) and the f16
+//     of the remainder x - f16(x) (rows 16..31), so the products carry ~22 bits of x;
+//   * the min term is one more MFMA per super-block: activation rows S_s / 32 (hi and lo parts,
+//     the division keeps S within f16 range for any |x| < 65504), weight columns 32 * m_s.
+// The f32 result of a super-block is scaled by d and dmin of the lane's row and accumulated;
+// the hi and lo rows of a token are added at the end.
+//
+// Work split: a workgroup = 4 waves x 64 rows (16 tiled records of 16 rows) over one K range of
+// the weight; K is split into SK ranges of about 4 super-blocks across workgroups, and a second
+// kernel adds the SK partial results in range order (deterministic). Each
+// wave streams its 4 records per super-block straight into registers (two super-blocks in
+// flight); the activation operands of a super-block (17 KB, L2-resident) are shared by the 4
+// waves through LDS, loaded with global_load_lds one super-block ahead.
+#include "kernels.hpp"
+
+namespace fhip {
+namespace {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ uint32_t as_u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+constexpr int kUnitsSB = 17;       // operand units (64 lanes x 16 B) per super-block: 16 + S
+constexpr int kTilesWG = 16;       // 16-row tiles per workgroup (4 waves x 64 rows)
+
+// Operand prep. xa[(b * 17 + s) * 64 + l]:
+//   s < 16: 8 f16 of operand row v = l & 31 at K = 256 b + 16 s + 8 (l >> 5) + perm8(j): the
+//           f16 of x[v] for v < 16, of x[v - 16] - f16(x[v - 16]) for v >= 16;
+//   s = 16: for l < 32, element j = the hi (v < 16) or lo part of S[t][perm8(j)] / 32, the f32
+//           sum of sub-block perm8(j) of super-block b in K order; zero for l >= 32.
+// Tokens >= M are zero.
+__global__ void gemv16_xprep_kernel(const float *__restrict__ X, int M, int K, int total,
+                                    uint4 *__restrict__ xa) {
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  const int l = id & 63, u = id >> 6;
+  const int b = u / kUnitsSB, s = u - b * kUnitsSB;
+  const int v = l & 31, t = v & 15;
+  const bool lo = v >= 16;
+  f16x8 h;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) h[j] = (_Float16)0.f;
+  if (t < M) {
+    const float *x = X + (size_t)t * K + 256 * (size_t)b;
+    if (s < 16) {
+      const float *p = x + 16 * s + 8 * (l >> 5);
+      const float4 v0 = *reinterpret_cast<const float4 *>(p);
+      const float4 v1 = *reinterpret_cast<const float4 *>(p + 4);
+      const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float xv = f[perm8(j)];
+        const _Float16 hi = (_Float16)xv;
+        h[j] = lo ? (_Float16)(xv - (float)hi) : hi;
+      }
+    } else if (l < 32) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float4 *p = reinterpret_cast<const float4 *>(x + 32 * perm8(j));
+        float S = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float4 q = p[k];
+          S += q.x;
+          S += q.y;
+          S += q.z;
+          S += q.w;
+        }
+        S *= 0.03125f;  // exact: a power of two
+        const _Float16 hi = (_Float16)S;
+        h[j] = lo ? (_Float16)(S - (float)hi) : hi;
+      }
+    }
+  }
+  xa[id] = __builtin_bit_cast(uint4, h);
+}
+
+// s_waitcnt immediate for vmcnt(n) with lgkmcnt(0); see q4k_gemm32.hip for the bare barrier.
+constexpr int wait_vm16(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
+#define FHIP_LDS_BARRIER16(imm)      \
+  do {                               \
+    __builtin_amdgcn_s_waitcnt(imm); \
+    asm volatile("" ::: "memory");   \
+    __builtin_amdgcn_s_barrier();    \
+    asm volatile("" ::: "memory");   \
+  } while (0)
+
+// One super-block's weight data of a lane: for each of its two 32-row MFMA tiles the 16-byte
+// header of its row and the four 16-byte nibble units it takes operands from.
+struct W16 {
+  uint4 hd[2];
+  uint4 nb[2][2][2];  // [tile][K half hh][lane group h]
+};
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4k_gemv16_kernel(
+    const uint8_t *__restrict__ W, const uint4 *__restrict__ xa, float *__restrict__ Y,
+    float *__restrict__ part, int N, int M, int nblk, int ntiles, int SK) {
+  // Two named stage buffers (the compiler tracks LDS DMA per object).
+  __shared__ u32x4 As0[kUnitsSB * 64];
+  __shared__ u32x4 As1[kUnitsSB * 64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kap = lane >> 5, rho = lane & 31, r16 = rho & 15;
+  const int rb = blockIdx.x / SK, sp = blockIdx.x - rb * SK;
+  const int kb0 = sp * nblk / SK, kb1 = (sp + 1) * nblk / SK;  // >= 1 super-block: SK <= nblk
+  const int nb = kb1 - kb0;
+  // This lane's two row tiles (row rho of a 32-row MFMA tile = row rho % 16 of 16-row tile
+  // rho / 16); loads use the last tile in place of ones past the end.
+  int Tt[2];
+  const uint8_t *rec[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    Tt[t] = kTilesWG * rb + 4 * wave + 2 * t + (rho >> 4);
+    rec[t] = W + (size_t)min(Tt[t], ntiles - 1) * nblk * kQ4kRecord;
+  }
+  auto load_w = [&](int b, W16 &o) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint8_t *r = rec[t] + (size_t)b * kQ4kRecord;
+      o.hd[t] = *reinterpret_cast<const uint4 *>(r + 16 * r16);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          o.nb[t][hh][h] = *reinterpret_cast<const uint4 *>(r + kQ4kHdr + 1024 * hh +
+                                                            16 * (16 * (2 * h + kap) + r16));
+    }
+  };
+  // Units w, w + 4, w + 8, w + 12 and the S unit (loaded by every wave: the same bytes to the
+  // same place), so each wave issues five loads per stage.
+  auto load_a = [&](int b, u32x4 *dst) {
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(xa) + (size_t)b * kUnitsSB * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+      const int unit = j < 4 ? wave + 4 * j : 16;
+      __builtin_amdgcn_global_load_lds((const void *)(src + unit * 64),
+                                       (__attribute__((address_space(3))) void *)(dst + unit * 64),
+                                       16, 0, 0);
+    }
+  };
+  auto buf = [&](int k) -> u32x4 * { return k == 0 ? As0 : As1; };
+
+  const uint32_t kLo = in_reg(0x000F000Fu), kHi = in_reg(0x00F000F0u);
+  const uint32_t kMagic = in_reg(0x64006400u), kB02 = in_reg(0x00FF00FFu);
+  const h2 k1024 = {(_Float16)1024.f, (_Float16)1024.f};
+  const h2 kN1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+  const h2 k16th = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const h2 k32 = {(_Float16)32.f, (_Float16)32.f};
+
+  f32x16 acc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[t][e] = 0.f;
+
+  W16 wr[2];
+  load_w(kb0, wr[0]);
+  load_w(min(kb0 + 1, kb1 - 1), wr[1]);
+  load_a(kb0, As0);
+  FHIP_LDS_BARRIER16(wait_vm16(0));
+
+  // Passes of two super-blocks (stage buffer and weight slot u are compile-time). Every pass
+  // issues the same loads (indices clamped) and reaches the same barrier; a pass past the end of
+  // the range computes on its clamped copy with d = dmin = 0, so the loop has no branch and
+  // each wait below is an exact count.
+  const int nbp = (nb + 1) & ~1;
+  for (int i0 = 0; i0 < nbp; i0 += 2) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = i0 + u;
+      const int b = kb0 + i;
+      // This slot's records (issued two passes ago) are older than the 10 loads of the other
+      // slot: the wait makes that explicit for the compiler, which otherwise drains everything.
+      __builtin_amdgcn_s_waitcnt(wait_vm16(10));
+      load_a(min(b + 1, kb1 - 1), buf(u ^ 1));
+      const u32x4 *Ab = buf(u);
+      W16 &cw = wr[u];
+      const float live = i < nb ? 1.f : 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint4 hd = cw.hd[t];
+        const float d = live * (float)__builtin_bit_cast(_Float16, (uint16_t)(hd.x & 0xffffu));
+        const float dm = live * (float)__builtin_bit_cast(_Float16, (uint16_t)(hd.x >> 16));
+        const uint32_t scl = hd.y & 0x3F3F3F3Fu, mnl = hd.z & 0x3F3F3F3Fu;
+        const uint32_t sch = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+        const uint32_t mnh = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+        // (sc_0, sc_2), (sc_1, sc_3), (sc_4, sc_6), (sc_5, sc_7) as exact f16 pairs.
+        const h2 e0 = as_h2((scl & kB02) | kMagic) - k1024;
+        const h2 o0 = as_h2(((scl >> 8) & kB02) | kMagic) - k1024;
+        const h2 e1 = as_h2((sch & kB02) | kMagic) - k1024;
+        const h2 o1 = as_h2(((sch >> 8) & kB02) | kMagic) - k1024;
+        // Min operand: element j = 32 m_perm8(j) for the lanes of K half 0, zero for half 1.
+        u32x4 mw;
+        mw[0] = as_u((as_h2((mnl & kB02) | kMagic) - k1024) * k32);
+        mw[1] = as_u((as_h2(((mnl >> 8) & kB02) | kMagic) - k1024) * k32);
+        mw[2] = as_u((as_h2((mnh & kB02) | kMagic) - k1024) * k32);
+        mw[3] = as_u((as_h2(((mnh >> 8) & kB02) | kMagic) - k1024) * k32);
+        if (kap) mw = u32x4{0u, 0u, 0u, 0u};
+
+        f32x16 tmp;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tmp[e] = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const h2 ep = c < 2 ? e0 : e1, op = c < 2 ? o0 : o1;
+          const _Float16 sa = (c & 1) ? ep.y : ep.x;  // sc of sub-block 2c (low nibbles)
+          const _Float16 sb = (c & 1) ? op.y : op.x;  // sc of sub-block 2c + 1 (high nibbles)
+          const h2 SL = {sa, sa}, SH = h2{sb, sb} * k16th;
+          const h2 NL = SL * kN1024, NH = SH * kN1024;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint4 q = cw.nb[t][c >> 1][h];
+            const uint32_t x0 = (c & 1) ? q.z : q.x, x1 = (c & 1) ? q.w : q.y;
+            const uint32_t y0 = x0 >> 8, y1 = x1 >> 8;
+            u32x4 lw, hw;
+            lw[0] = as_u(__builtin_elementwise_fma(as_h2((x0 & kLo) | kMagic), SL, NL));
+            lw[1] = as_u(__builtin_elementwise_fma(as_h2((y0 & kLo) | kMagic), SL, NL));
+            lw[2] = as_u(__builtin_elementwise_fma(as_h2((x1 & kLo) | kMagic), SL, NL));
+            lw[3] = as_u(__builtin_elementwise_fma(as_h2((y1 & kLo) | kMagic), SL, NL));
+            hw[0] = as_u(__builtin_elementwise_fma(as_h2((x0 & kHi) | kMagic), SH, NH));
+            hw[1] = as_u(__builtin_elementwise_fma(as_h2((y0 & kHi) | kMagic), SH, NH));
+            hw[2] = as_u(__builtin_elementwise_fma(as_h2((x1 & kHi) | kMagic), SH, NH));
+            hw[3] = as_u(__builtin_elementwise_fma(as_h2((y1 & kHi) | kMagic), SH, NH));
+            const f16x8 bl = __builtin_bit_cast(f16x8, lw), bh = __builtin_bit_cast(f16x8, hw);
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi) {
+              const f16x8 a = __builtin_bit_cast(f16x8, Ab[(4 * c + 2 * hi + h) * 64 + lane]);
+              tmp = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, hi ? bh : bl, tmp, 0, 0, 0);
+            }
+          }
+        }
+        f32x16 mt;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mt[e] = 0.f;
+        mt = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, Ab[16 * 64 + lane]),
+                                                    __builtin_bit_cast(f16x8, mw), mt, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[t][e] = fmaf(d, tmp[e], fmaf(-dm, mt[e], acc[t][e]));
+      }
+      load_w(min(b + 2, kb1 - 1), cw);
+      // Stage b + 1 has landed once at most 10 of this wave's later loads (the records of
+      // b + 2) are pending.
+      FHIP_LDS_BARRIER16(wait_vm16(10));
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(wait_vm16(0));  // no LDS DMA may be pending when the workgroup ends
+
+  // D layout: lane (kap, rho) holds column rho and operand rows 8 (e / 4) + 4 kap + e % 4:
+  // e < 8 the hi rows of tokens 8 (e / 4) + 4 kap + e % 4, e + 8 the lo rows of the same tokens.
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int row = 16 * Tt[t] + r16;
+    if (row >= N) continue;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tok = 8 * (e >> 2) + 4 * kap + (e & 3);
+      if (tok >= M) continue;
+      const float v = acc[t][e] + acc[t][e + 8];
+      if (SK == 1)
+        Y[(size_t)tok * N + row] = v;
+      else
+        part[((size_t)sp * M + tok) * N + row] = v;
+    }
+  }
+}
+#undef FHIP_LDS_BARRIER16
+
+// Y = sum of the SK partial results in range order: four outputs per thread when M * N is a
+// multiple of 4 and Y 16-byte aligned, else one.
+__global__ void gemv16_reduce1_kernel(const float *__restrict__ part, float *__restrict__ Y,
+                                      int SK, int total) {
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  float v = part[id];
+  for (int s = 1; s < SK; ++s) v += part[(size_t)s * total + id];
+  Y[id] = v;
+}
+
+__global__ void gemv16_reduce_kernel(const float4 *__restrict__ part, float4 *__restrict__ Y,
+                                     int SK, int total4) {
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total4) return;
+  float4 v = part[id];
+  for (int s = 1; s < SK; ++s) {
+    const float4 p = part[(size_t)s * total4 + id];
+    v.x += p.x;
+    v.y += p.y;
+    v.z += p.z;
+    v.w += p.w;
+  }
+  Y[id] = v;
+}
+
+}  // namespace
+
+// K ranges per call: ranges of 4 super-blocks when K allows it, else of 4 to 5 (the kernel
+// works in passes of two super-blocks, so an odd range pads one; measured at the 7B / 27B FFN
+// shapes at 16 tokens, longer ranges lose parallelism and shorter ones pay more per-range start
+// and partial-sum traffic). FAK_HIP_GEMV16_SK overrides (tuning).
+int gemv16_splits(int nblk) {
+  int sk = env_int("FAK_HIP_GEMV16_SK");
+  if (sk <= 0) sk = nblk % 4 == 0 ? nblk / 4 : (int)(nblk / 4.6);
+  if (sk < 1) sk = 1;
+  if (sk > nblk) sk = nblk;
+  return sk;
+}
+
+int q4k_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
+  if (M < 1 || M > 16) return fail(FHIP_EINVAL, "q4k_gemv16: M=%d outside 1..16", M);
+  const int nblk = K / 256, ntiles = q4k_tiles(N);
+  const int nrb = ceil_div(ntiles, kTilesWG);
+  const int SK = gemv16_splits(nblk);
+  const size_t xab = (size_t)nblk * kUnitsSB * 64 * 16;
+  const size_t pb = SK > 1 ? (size_t)SK * M * N * 4 : 0;
+  unsigned char *ws = (unsigned char *)workspace(xab + pb);
+  if (!ws) return FHIP_ENOMEM;
+  const int total = nblk * kUnitsSB * 64;
+  gemv16_xprep_kernel<<<ceil_div(total, 256), 256, 0, stream()>>>(X, M, K, total, (uint4 *)ws);
+  FHIP_CHECK_LAUNCH("gemv16_xprep_kernel");
+  float *part = SK > 1 ? (float *)(ws + xab) : nullptr;
+  q4k_gemv16_kernel<<<nrb * SK, 256, 0, stream()>>>((const uint8_t *)Wv, (const uint4 *)ws, Y,
+                                                     part, N, M, nblk, ntiles, SK);
+  FHIP_CHECK_LAUNCH("q4k_gemv16_kernel");
+  if (SK > 1) {
+    const int tot = M * N;
+    if (tot % 4 == 0 && ((uintptr_t)Y & 15) == 0)
+      gemv16_reduce_kernel<<<ceil_div(tot / 4, 256), 256, 0, stream()>>>(
+          (const float4 *)part, (float4 *)Y, SK, tot / 4);
+    else
+      gemv16_reduce1_kernel<<<ceil_div(tot, 256), 256, 0, stream()>>>(part, Y, SK, tot);
+    FHIP_CHECK_LAUNCH("gemv16_reduce_kernel");
+  }
+  return FHIP_OK;
+}
+
+}  // namespace fhip
