@@ -17,10 +17,10 @@
 //
 // Work split: a workgroup = 4 waves x 64 rows (16 tiled records of 16 rows) over one K range of
 // the weight; K is split into SK ranges of about 4 super-blocks across workgroups, and a second
-// kernel adds the SK partial results in range order (deterministic). Each
-// wave streams its 4 records per super-block straight into registers (two super-blocks in
-// flight); the activation operands of a super-block (17 KB, L2-resident) are shared by the 4
-// waves through LDS, loaded with global_load_lds one super-block ahead.
+// kernel adds the SK partial results in range order (deterministic). Each wave streams its 4
+// records per super-block straight into registers (two super-blocks in flight). The workgroup
+// builds the activation operands of each super-block itself, one super-block ahead, from X
+// (16 KB of f32, L2-resident) into an LDS stage shared by its 4 waves: no separate prep launch.
 #include "kernels.hpp"
 
 namespace fhip {
@@ -32,60 +32,15 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 __device__ __forceinline__ uint32_t as_u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 
-constexpr int kUnitsSB = 17;       // operand units (64 lanes x 16 B) per super-block: 16 + S
 constexpr int kTilesWG = 16;       // 16-row tiles per workgroup (4 waves x 64 rows)
 
-// Operand prep. xa[(b * 17 + s) * 64 + l]:
-//   s < 16: 8 f16 of operand row v = l & 31 at K = 256 b + 16 s + 8 (l >> 5) + perm8(j): the
-//           f16 of x[v] for v < 16, of x[v - 16] - f16(x[v - 16]) for v >= 16;
-//   s = 16: for l < 32, element j = the hi (v < 16) or lo part of S[t][perm8(j)] / 32, the f32
-//           sum of sub-block perm8(j) of super-block b in K order; zero for l >= 32.
+// LDS stage of one super-block b: 17 units of 64 lanes x 16 B.
+//   unit s < 16, lane l: 8 f16 of operand row v = l & 31 at K = 256 b + 16 s + 8 (l >> 5) +
+//     perm8(j): the f16 of x[v] for v < 16, of x[v - 16] - f16(x[v - 16]) for v >= 16;
+//   unit 16, lane l < 32: element j = the hi (v < 16) or lo part of S[t][perm8(j)] / 32, the f32
+//     sum of sub-block perm8(j) of b; lanes >= 32 zero.
 // Tokens >= M are zero.
-__global__ void gemv16_xprep_kernel(const float *__restrict__ X, int M, int K, int total,
-                                    uint4 *__restrict__ xa) {
-  const int id = blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= total) return;
-  const int l = id & 63, u = id >> 6;
-  const int b = u / kUnitsSB, s = u - b * kUnitsSB;
-  const int v = l & 31, t = v & 15;
-  const bool lo = v >= 16;
-  f16x8 h;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) h[j] = (_Float16)0.f;
-  if (t < M) {
-    const float *x = X + (size_t)t * K + 256 * (size_t)b;
-    if (s < 16) {
-      const float *p = x + 16 * s + 8 * (l >> 5);
-      const float4 v0 = *reinterpret_cast<const float4 *>(p);
-      const float4 v1 = *reinterpret_cast<const float4 *>(p + 4);
-      const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float xv = f[perm8(j)];
-        const _Float16 hi = (_Float16)xv;
-        h[j] = lo ? (_Float16)(xv - (float)hi) : hi;
-      }
-    } else if (l < 32) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float4 *p = reinterpret_cast<const float4 *>(x + 32 * perm8(j));
-        float S = 0.f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const float4 q = p[k];
-          S += q.x;
-          S += q.y;
-          S += q.z;
-          S += q.w;
-        }
-        S *= 0.03125f;  // exact: a power of two
-        const _Float16 hi = (_Float16)S;
-        h[j] = lo ? (_Float16)(S - (float)hi) : hi;
-      }
-    }
-  }
-  xa[id] = __builtin_bit_cast(uint4, h);
-}
+constexpr int kUnitsSB = 17;
 
 // s_waitcnt immediate for vmcnt(n) with lgkmcnt(0); see q4k_gemm32.hip for the bare barrier.
 constexpr int wait_vm16(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
@@ -105,9 +60,9 @@ struct W16 {
 };
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4k_gemv16_kernel(
-    const uint8_t *__restrict__ W, const uint4 *__restrict__ xa, float *__restrict__ Y,
-    float *__restrict__ part, int N, int M, int nblk, int ntiles, int SK) {
-  // Two named stage buffers (the compiler tracks LDS DMA per object).
+    const uint8_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y,
+    float *__restrict__ part, int N, int K, int M, int nblk, int ntiles, int SK) {
+  // Two stage buffers: the one being read and the one being built.
   __shared__ u32x4 As0[kUnitsSB * 64];
   __shared__ u32x4 As1[kUnitsSB * 64];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -118,13 +73,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int nb = kb1 - kb0;
   // This lane's two row tiles (row rho of a 32-row MFMA tile = row rho % 16 of 16-row tile
   // rho / 16); loads use the last tile in place of ones past the end.
-  int Tt[2];
+  auto tile_of = [&](int t) { return kTilesWG * rb + 4 * wave + 2 * t + (rho >> 4); };
   const uint8_t *rec[2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    Tt[t] = kTilesWG * rb + 4 * wave + 2 * t + (rho >> 4);
-    rec[t] = W + (size_t)min(Tt[t], ntiles - 1) * nblk * kQ4kRecord;
-  }
+  for (int t = 0; t < 2; ++t)
+    rec[t] = W + (size_t)min(tile_of(t), ntiles - 1) * nblk * kQ4kRecord;
   auto load_w = [&](int b, W16 &o) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -138,17 +91,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                                             16 * (16 * (2 * h + kap) + r16));
     }
   };
-  // Units w, w + 4, w + 8, w + 12 and the S unit (loaded by every wave: the same bytes to the
-  // same place), so each wave issues five loads per stage.
-  auto load_a = [&](int b, u32x4 *dst) {
-    const u32x4 *src = reinterpret_cast<const u32x4 *>(xa) + (size_t)b * kUnitsSB * 64 + lane;
+  // Stage building: thread (t, sb, half) = tid (16 x 8 x 2) owns the 16 activations of token t
+  // at K = 256 b + 32 sb + 16 half (two 8-runs). The loads go out at the start of a pass and are
+  // turned into operands at its end, after the MFMA work.
+  const int xt = tid >> 4, xsb = (tid >> 1) & 7, xhalf = tid & 1;
+  const bool xvalid = xt < M;
+  const float4 *xrow = reinterpret_cast<const float4 *>(X + (size_t)(xvalid ? xt : 0) * K +
+                                                        32 * xsb + 16 * xhalf);
+  auto load_x = [&](int b, float4 (&xv)[4]) {
 #pragma unroll
-    for (int j = 0; j < 5; ++j) {
-      const int unit = j < 4 ? wave + 4 * j : 16;
-      __builtin_amdgcn_global_load_lds((const void *)(src + unit * 64),
-                                       (__attribute__((address_space(3))) void *)(dst + unit * 64),
-                                       16, 0, 0);
+    for (int q = 0; q < 4; ++q)
+      xv[q] = xvalid ? xrow[64 * (size_t)b + q] : float4{0.f, 0.f, 0.f, 0.f};
+  };
+  auto store_x = [&](const float4 (&xv)[4], u32x4 *dst) {
+    const float f[16] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w,
+                         xv[2].x, xv[2].y, xv[2].z, xv[2].w, xv[3].x, xv[3].y, xv[3].z, xv[3].w};
+    float ps = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ps += f[k];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // 8-run i: K16 slice 2 xsb + xhalf, lane group i
+      f16x8 hv, lv;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float xv1 = f[8 * i + perm8(j)];
+        const _Float16 hi = (_Float16)xv1;
+        hv[j] = hi;
+        lv[j] = (_Float16)(xv1 - (float)hi);
+      }
+      u32x4 *unit = dst + (2 * xsb + xhalf) * 64 + 32 * i;
+      unit[xt] = __builtin_bit_cast(u32x4, hv);
+      unit[16 + xt] = __builtin_bit_cast(u32x4, lv);
     }
+    // Sub-block sum = the two halves' partial sums (neighbour lanes), in half order.
+    const float other = __shfl_xor(ps, 1);
+    const float S = (xhalf ? other + ps : ps + other) * 0.03125f;  // exact: a power of two
+    const _Float16 Sh = (_Float16)S;
+    _Float16 *su = reinterpret_cast<_Float16 *>(dst + 16 * 64);
+    const int j = perm8(xsb);  // perm8 is its own inverse
+    if (xhalf == 0)
+      su[xt * 8 + j] = Sh;
+    else
+      su[(16 + xt) * 8 + j] = (_Float16)(S - (float)Sh);
   };
   auto buf = [&](int k) -> u32x4 * { return k == 0 ? As0 : As1; };
 
@@ -166,9 +150,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int e = 0; e < 16; ++e) acc[t][e] = 0.f;
 
   W16 wr[2];
+  float4 xv[4];
+  load_x(kb0, xv);
   load_w(kb0, wr[0]);
   load_w(min(kb0 + 1, kb1 - 1), wr[1]);
-  load_a(kb0, As0);
+  if (tid < 64) {  // lanes 32..63 of both S units: zero for the whole kernel
+    const int k = tid & 31;
+    (tid < 32 ? As0 : As1)[16 * 64 + 32 + k] = u32x4{0u, 0u, 0u, 0u};
+  }
+  store_x(xv, As0);
   FHIP_LDS_BARRIER16(wait_vm16(0));
 
   // Passes of two super-blocks (stage buffer and weight slot u are compile-time). Every pass
@@ -184,7 +174,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // This slot's records (issued two passes ago) are older than the 10 loads of the other
       // slot: the wait makes that explicit for the compiler, which otherwise drains everything.
       __builtin_amdgcn_s_waitcnt(wait_vm16(10));
-      load_a(min(b + 1, kb1 - 1), buf(u ^ 1));
+      load_x(min(b + 1, kb1 - 1), xv);
       const u32x4 *Ab = buf(u);
       W16 &cw = wr[u];
       const float live = i < nb ? 1.f : 0.f;
@@ -250,18 +240,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int e = 0; e < 16; ++e) acc[t][e] = fmaf(d, tmp[e], fmaf(-dm, mt[e], acc[t][e]));
       }
       load_w(min(b + 2, kb1 - 1), cw);
-      // Stage b + 1 has landed once at most 10 of this wave's later loads (the records of
-      // b + 2) are pending.
+      // The activations of b + 1 have landed once at most 10 of this wave's later loads (the
+      // records of b + 2) are pending; the stage they make is visible after the barrier.
+      __builtin_amdgcn_s_waitcnt(wait_vm16(10));
+      store_x(xv, buf(u ^ 1));
       FHIP_LDS_BARRIER16(wait_vm16(10));
     }
   }
-  __builtin_amdgcn_s_waitcnt(wait_vm16(0));  // no LDS DMA may be pending when the workgroup ends
-
   // D layout: lane (kap, rho) holds column rho and operand rows 8 (e / 4) + 4 kap + e % 4:
   // e < 8 the hi rows of tokens 8 (e / 4) + 4 kap + e % 4, e + 8 the lo rows of the same tokens.
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int row = 16 * Tt[t] + r16;
+    const int row = 16 * tile_of(t) + (lane & 15);  // recomputed: not kept live in the loop
     if (row >= N) continue;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -322,16 +312,13 @@ int q4k_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
   const int nblk = K / 256, ntiles = q4k_tiles(N);
   const int nrb = ceil_div(ntiles, kTilesWG);
   const int SK = gemv16_splits(nblk);
-  const size_t xab = (size_t)nblk * kUnitsSB * 64 * 16;
-  const size_t pb = SK > 1 ? (size_t)SK * M * N * 4 : 0;
-  unsigned char *ws = (unsigned char *)workspace(xab + pb);
-  if (!ws) return FHIP_ENOMEM;
-  const int total = nblk * kUnitsSB * 64;
-  gemv16_xprep_kernel<<<ceil_div(total, 256), 256, 0, stream()>>>(X, M, K, total, (uint4 *)ws);
-  FHIP_CHECK_LAUNCH("gemv16_xprep_kernel");
-  float *part = SK > 1 ? (float *)(ws + xab) : nullptr;
-  q4k_gemv16_kernel<<<nrb * SK, 256, 0, stream()>>>((const uint8_t *)Wv, (const uint4 *)ws, Y,
-                                                     part, N, M, nblk, ntiles, SK);
+  float *part = nullptr;
+  if (SK > 1) {
+    part = (float *)workspace((size_t)SK * M * N * 4);
+    if (!part) return FHIP_ENOMEM;
+  }
+  q4k_gemv16_kernel<<<nrb * SK, 256, 0, stream()>>>((const uint8_t *)Wv, X, Y, part, N, K, M,
+                                                     nblk, ntiles, SK);
   FHIP_CHECK_LAUNCH("q4k_gemv16_kernel");
   if (SK > 1) {
     const int tot = M * N;
