@@ -191,13 +191,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const h2 o0 = as_h2(((scl >> 8) & kB02) | kMagic) - k1024;
         const h2 e1 = as_h2((sch & kB02) | kMagic) - k1024;
         const h2 o1 = as_h2(((sch >> 8) & kB02) | kMagic) - k1024;
-        // Min operand: element j = 32 m_perm8(j) for the lanes of K half 0, zero for half 1.
+        // Min operand: element j = 32 m_perm8(j) (every lane: the activation S unit is zero in
+        // the lanes of K half 1, so those products vanish).
         u32x4 mw;
         mw[0] = as_u((as_h2((mnl & kB02) | kMagic) - k1024) * k32);
         mw[1] = as_u((as_h2(((mnl >> 8) & kB02) | kMagic) - k1024) * k32);
         mw[2] = as_u((as_h2((mnh & kB02) | kMagic) - k1024) * k32);
         mw[3] = as_u((as_h2(((mnh >> 8) & kB02) | kMagic) - k1024) * k32);
-        if (kap) mw = u32x4{0u, 0u, 0u, 0u};
 
         f32x16 tmp;
 #pragma unroll
@@ -249,6 +249,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   // D layout: lane (kap, rho) holds column rho and operand rows 8 (e / 4) + 4 kap + e % 4:
   // e < 8 the hi rows of tokens 8 (e / 4) + 4 kap + e % 4, e + 8 the lo rows of the same tokens.
+  float v[2][8];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[t][e] = acc[t][e] + acc[t][e + 8];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int row = 16 * tile_of(t) + (lane & 15);  // recomputed: not kept live in the loop
@@ -257,11 +262,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int e = 0; e < 8; ++e) {
       const int tok = 8 * (e >> 2) + 4 * kap + (e & 3);
       if (tok >= M) continue;
-      const float v = acc[t][e] + acc[t][e + 8];
       if (SK == 1)
-        Y[(size_t)tok * N + row] = v;
+        Y[(size_t)tok * N + row] = v[t][e];
       else
-        part[((size_t)sp * M + tok) * N + row] = v;
+        part[((size_t)sp * M + tok) * N + row] = v[t][e];
     }
   }
 }
