@@ -316,6 +316,9 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
     for (int u = 0; u < PF; ++u) {
       const int b = bb + u;
       if (b >= b1) break;
+      // This slot's three loads are older than the other slots' refills: saying so lets the
+      // compiler wait for just this record instead of draining the ring at the top of a pass.
+      if (LX) __builtin_amdgcn_s_waitcnt(0x0F70 | (3 * (PF - 1)));
       Ops &cur = ring[u];
 
       float4 es[MP];
