@@ -1,4 +1,5 @@
-// q4k_gemv16.hip — Q4_K matmul for 5..16 tokens (speculative verify) on the 32x32x16 f16 MFMA.
+// q4k_gemv16.hip — Q4_K (and Q6_K) matmul for 5..16 tokens (speculative verify) on the
+// 32x32x16 f16 MFMA.
 //
 // Y[t][o] = sum_k W[o][k] X[t][k] with W the Q4_K weight (w = d*sc_s*n - dmin*m_s per 32-weight
 // sub-block s, internal/model/quant_q4k.go:90-111). Per super-block b of row o and token t
@@ -21,6 +22,13 @@
 // records per super-block straight into registers (two super-blocks in flight). The workgroup
 // builds the activation operands of each super-block itself, one super-block ahead, from X
 // (16 KB of f32, L2-resident) into an LDS stage shared by its 4 waves: no separate prep launch.
+//
+// Q6_K weights (w = d * sc_g * (q - 32) per 16-weight group g, internal/model/quant_kquant.go
+// :139-163) run the same kernel with one 32-row tile per wave (their records need more
+// registers): the K16 slice g of a super-block is group g, the integer sc_g * (q - 32) (up to
+// 4096 in magnitude, more than f16 holds exactly) is the sum of two exact f16 operands, f16 of
+// it and the remainder, fed to two MFMAs; there is no min term, and the f32 result of a
+// super-block is scaled by d.
 #include "kernels.hpp"
 
 namespace fhip {
@@ -32,7 +40,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 __device__ __forceinline__ uint32_t as_u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 
-constexpr int kTilesWG = 16;       // 16-row tiles per workgroup (4 waves x 64 rows)
 
 // LDS stage of one super-block b: 17 units of 64 lanes x 16 B.
 //   unit s < 16, lane l: 8 f16 of operand row v = l & 31 at K = 256 b + 16 s + 8 (l >> 5) +
@@ -52,14 +59,28 @@ constexpr int wait_vm16(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
     asm volatile("" ::: "memory");   \
   } while (0)
 
-// One super-block's weight data of a lane: for each of its two 32-row MFMA tiles the 16-byte
-// header of its row and the four 16-byte nibble units it takes operands from.
-struct W16 {
+// One super-block's weight data of a lane.
+// Q4_K (two 32-row MFMA tiles per wave): per tile the 16-byte header of the lane's row and the
+// four 16-byte nibble units it takes operands from.
+// Q6_K (one tile per wave): the row's 16 int8 scales, its d, and for each K half hh and lane
+// group h the 8 ql bytes of groups 4c + h and 4c + 2 + h (c = 2 hh, 2 hh + 1: low and high
+// nibble) and their 8 qh bytes.
+template <int FMT>
+struct W16;
+template <>
+struct W16<0> {
   uint4 hd[2];
   uint4 nb[2][2][2];  // [tile][K half hh][lane group h]
 };
+template <>
+struct W16<1> {
+  uint4 sc;
+  uint32_t d;
+  uint2 q[2][2][3];  // [K half hh][lane group h][ql a, ql b, qh]
+};
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4k_gemv16_kernel(
+template <int FMT>  // 0: Q4_K, 1: Q6_K
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void quant_gemv16_kernel(
     const uint8_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y,
     float *__restrict__ part, int N, int K, int M, int nblk, int ntiles, int SK) {
   // Two stage buffers: the one being read and the one being built.
@@ -71,24 +92,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int rb = blockIdx.x / SK, sp = blockIdx.x - rb * SK;
   const int kb0 = sp * nblk / SK, kb1 = (sp + 1) * nblk / SK;  // >= 1 super-block: SK <= nblk
   const int nb = kb1 - kb0;
-  // This lane's two row tiles (row rho of a 32-row MFMA tile = row rho % 16 of 16-row tile
+  constexpr int NT = FMT == 0 ? 2 : 1;           // 32-row MFMA tiles per wave
+  constexpr int TWG = 8 * NT;                      // 16-row tiles per workgroup
+  constexpr int kRec = FMT == 0 ? kQ4kRecord : kQ6kRecord;
+  constexpr int kWL = FMT == 0 ? 10 : 14;          // record loads per super-block per lane
+  // This lane's row tiles (row rho of a 32-row MFMA tile = row rho % 16 of 16-row tile
   // rho / 16); loads use the last tile in place of ones past the end.
-  auto tile_of = [&](int t) { return kTilesWG * rb + 4 * wave + 2 * t + (rho >> 4); };
-  const uint8_t *rec[2];
+  auto tile_of = [&](int t) { return TWG * rb + 2 * NT * wave + 2 * t + (rho >> 4); };
+  const uint8_t *rec[NT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
-    rec[t] = W + (size_t)min(tile_of(t), ntiles - 1) * nblk * kQ4kRecord;
-  auto load_w = [&](int b, W16 &o) {
+  for (int t = 0; t < NT; ++t)
+    rec[t] = W + (size_t)min(tile_of(t), ntiles - 1) * nblk * kRec;
+  auto load_w = [&](int b, W16<FMT> &o) {
+    if constexpr (FMT == 0) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint8_t *r = rec[t] + (size_t)b * kQ4kRecord;
-      o.hd[t] = *reinterpret_cast<const uint4 *>(r + 16 * r16);
+      for (int t = 0; t < NT; ++t) {
+        const uint8_t *r = rec[t] + (size_t)b * kRec;
+        o.hd[t] = *reinterpret_cast<const uint4 *>(r + 16 * r16);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            o.nb[t][hh][h] = *reinterpret_cast<const uint4 *>(r + kQ4kHdr + 1024 * hh +
+                                                              16 * (16 * (2 * h + kap) + r16));
+      }
+    } else {
+      const uint8_t *r = rec[0] + (size_t)b * kRec;
+      o.sc = *reinterpret_cast<const uint4 *>(r + 16 * r16);
+      o.d = *reinterpret_cast<const uint16_t *>(r + kQ6kD + 2 * r16);
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-          o.nb[t][hh][h] = *reinterpret_cast<const uint4 *>(r + kQ4kHdr + 1024 * hh +
-                                                            16 * (16 * (2 * h + kap) + r16));
+        for (int h = 0; h < 2; ++h) {
+          o.q[hh][h][0] = *reinterpret_cast<const uint2 *>(r + kQ6kQl + 1024 * hh +
+                                                           16 * (16 * h + r16) + 8 * kap);
+          o.q[hh][h][1] = *reinterpret_cast<const uint2 *>(r + kQ6kQl + 1024 * hh +
+                                                           16 * (16 * (2 + h) + r16) + 8 * kap);
+          o.q[hh][h][2] = *reinterpret_cast<const uint2 *>(r + kQ6kQh + 512 * hh + 256 * h +
+                                                           16 * r16 + 8 * kap);
+        }
     }
   };
   // Stage building: thread (t, sb, half) = tid (16 x 8 x 2) owns the 16 activations of token t
@@ -142,14 +184,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const h2 kN1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
   const h2 k16th = {(_Float16)0.0625f, (_Float16)0.0625f};
   const h2 k32 = {(_Float16)32.f, (_Float16)32.f};
+  const h2 k1056 = {(_Float16)1056.f, (_Float16)1056.f};
+  const uint32_t k0F = in_reg(0x0F0F0F0Fu), k03 = in_reg(0x03030303u);
 
-  f32x16 acc[2];
+  f32x16 acc[NT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[t][e] = 0.f;
 
-  W16 wr[2];
+  W16<FMT> wr[2];
   float4 xv[4];
   load_x(kb0, xv);
   load_w(kb0, wr[0]);
@@ -171,15 +215,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int u = 0; u < 2; ++u) {
       const int i = i0 + u;
       const int b = kb0 + i;
-      // This slot's records (issued two passes ago) are older than the 10 loads of the other
+      // This slot's records (issued two passes ago) are older than the kWL loads of the other
       // slot: the wait makes that explicit for the compiler, which otherwise drains everything.
-      __builtin_amdgcn_s_waitcnt(wait_vm16(10));
+      __builtin_amdgcn_s_waitcnt(wait_vm16(kWL));
       load_x(min(b + 1, kb1 - 1), xv);
       const u32x4 *Ab = buf(u);
-      W16 &cw = wr[u];
+      W16<FMT> &cw = wr[u];
       const float live = i < nb ? 1.f : 0.f;
+      if constexpr (FMT == 0) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < NT; ++t) {
         const uint4 hd = cw.hd[t];
         const float d = live * (float)__builtin_bit_cast(_Float16, (uint16_t)(hd.x & 0xffffu));
         const float dm = live * (float)__builtin_bit_cast(_Float16, (uint16_t)(hd.x >> 16));
@@ -239,23 +284,81 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[t][e] = fmaf(d, tmp[e], fmaf(-dm, mt[e], acc[t][e]));
       }
+      } else {
+        // Q6_K: w = d * sc_g * (q - 32) per 16-weight group g = K16 slice g. The integer
+        // sc_g * (q - 32) (up to 4096 in magnitude) goes in as two exact f16 operands; the f32
+        // result of the super-block is scaled by d.
+        const float d = live * (float)__builtin_bit_cast(_Float16, (uint16_t)(cw.d & 0xffffu));
+        const uint32_t scv[4] = {cw.sc.x, cw.sc.y, cw.sc.z, cw.sc.w};
+        f32x16 tmp;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tmp[e] = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int k = c & 1;  // nibble of ql, qh fields 4k (slice a) and 4k + 2 (slice b)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const _Float16 sa = (_Float16)(float)(int8_t)(scv[c] >> (8 * h));
+            const _Float16 sb = (_Float16)(float)(int8_t)(scv[c] >> (8 * (2 + h)));
+            const h2 SA = {sa, sa}, SB = {sb, sb};
+            const uint2 qa = cw.q[c >> 1][h][0], qb = cw.q[c >> 1][h][1], qh = cw.q[c >> 1][h][2];
+            const uint32_t qav[2] = {qa.x, qa.y}, qbv[2] = {qb.x, qb.y}, qhv[2] = {qh.x, qh.y};
+            // Operand = v_hi + v_lo with v = sc * (q - 32): v_hi = f16(v) and v_lo = v - v_hi
+            // (0 or +-1, from one fma with the exact product), so the pair is exact.
+            u32x4 ra, rbw, la, lbw;
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+              const uint32_t ca = ((qav[m] >> (4 * k)) & k0F) | (((qhv[m] >> (4 * k)) & k03) << 4);
+              const uint32_t cb =
+                  ((qbv[m] >> (4 * k)) & k0F) | (((qhv[m] >> (4 * k + 2)) & k03) << 4);
+              // bytes (0, 2) and (1, 3) of each code word: elements in perm8 order
+              const h2 qa0 = as_h2((ca & kB02) | kMagic) - k1056;
+              const h2 qa1 = as_h2(((ca >> 8) & kB02) | kMagic) - k1056;
+              const h2 qb0 = as_h2((cb & kB02) | kMagic) - k1056;
+              const h2 qb1 = as_h2(((cb >> 8) & kB02) | kMagic) - k1056;
+              const h2 va0 = qa0 * SA, va1 = qa1 * SA, vb0 = qb0 * SB, vb1 = qb1 * SB;
+              ra[2 * m] = as_u(va0);
+              ra[2 * m + 1] = as_u(va1);
+              rbw[2 * m] = as_u(vb0);
+              rbw[2 * m + 1] = as_u(vb1);
+              la[2 * m] = as_u(__builtin_elementwise_fma(qa0, SA, -va0));
+              la[2 * m + 1] = as_u(__builtin_elementwise_fma(qa1, SA, -va1));
+              lbw[2 * m] = as_u(__builtin_elementwise_fma(qb0, SB, -vb0));
+              lbw[2 * m + 1] = as_u(__builtin_elementwise_fma(qb1, SB, -vb1));
+            }
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi) {
+              const f16x8 a = __builtin_bit_cast(f16x8, Ab[(4 * c + 2 * hi + h) * 64 + lane]);
+              tmp = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                  a, __builtin_bit_cast(f16x8, hi ? rbw : ra), tmp, 0, 0, 0);
+              tmp = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                  a, __builtin_bit_cast(f16x8, hi ? lbw : la), tmp, 0, 0, 0);
+            }
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[0][e] = fmaf(d, tmp[e], acc[0][e]);
+      }
       load_w(min(b + 2, kb1 - 1), cw);
-      // The activations of b + 1 have landed once at most 10 of this wave's later loads (the
-      // records of b + 2) are pending; the stage they make is visible after the barrier.
-      __builtin_amdgcn_s_waitcnt(wait_vm16(10));
+      // The activations of b + 1 have landed once at most kWL of this wave's later loads (the
+      // records of b + 2) are pending; the stage they make is visible after the barrier. (The
+      // sched_barrier keeps their conversion below the record loads: hoisted into the MFMA
+      // work it would wait for the records of b + 1 too.)
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(wait_vm16(kWL));
       store_x(xv, buf(u ^ 1));
-      FHIP_LDS_BARRIER16(wait_vm16(10));
+      FHIP_LDS_BARRIER16(wait_vm16(kWL));
     }
   }
   // D layout: lane (kap, rho) holds column rho and operand rows 8 (e / 4) + 4 kap + e % 4:
   // e < 8 the hi rows of tokens 8 (e / 4) + 4 kap + e % 4, e + 8 the lo rows of the same tokens.
-  float v[2][8];
+  float v[NT][8];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[t][e] = acc[t][e] + acc[t][e + 8];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < NT; ++t) {
     const int row = 16 * tile_of(t) + (lane & 15);  // recomputed: not kept live in the loop
     if (row >= N) continue;
 #pragma unroll
@@ -311,19 +414,21 @@ int gemv16_splits(int nblk) {
   return sk;
 }
 
-int q4k_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
-  if (M < 1 || M > 16) return fail(FHIP_EINVAL, "q4k_gemv16: M=%d outside 1..16", M);
+namespace {
+template <int FMT>
+int launch_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
+  if (M < 1 || M > 16) return fail(FHIP_EINVAL, "gemv16: M=%d outside 1..16", M);
   const int nblk = K / 256, ntiles = q4k_tiles(N);
-  const int nrb = ceil_div(ntiles, kTilesWG);
+  const int nrb = ceil_div(ntiles, FMT == 0 ? 16 : 8);
   const int SK = gemv16_splits(nblk);
   float *part = nullptr;
   if (SK > 1) {
     part = (float *)workspace((size_t)SK * M * N * 4);
     if (!part) return FHIP_ENOMEM;
   }
-  q4k_gemv16_kernel<<<nrb * SK, 256, 0, stream()>>>((const uint8_t *)Wv, X, Y, part, N, K, M,
-                                                     nblk, ntiles, SK);
-  FHIP_CHECK_LAUNCH("q4k_gemv16_kernel");
+  quant_gemv16_kernel<FMT><<<nrb * SK, 256, 0, stream()>>>((const uint8_t *)Wv, X, Y, part, N, K,
+                                                            M, nblk, ntiles, SK);
+  FHIP_CHECK_LAUNCH("quant_gemv16_kernel");
   if (SK > 1) {
     const int tot = M * N;
     if (tot % 4 == 0 && ((uintptr_t)Y & 15) == 0)
@@ -334,6 +439,15 @@ int q4k_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
     FHIP_CHECK_LAUNCH("gemv16_reduce_kernel");
   }
   return FHIP_OK;
+}
+}  // namespace
+
+int q4k_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
+  return launch_gemv16<0>(Wv, X, Y, N, K, M);
+}
+
+int q6k_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
+  return launch_gemv16<1>(Wv, X, Y, N, K, M);
 }
 
 }  // namespace fhip

@@ -329,6 +329,9 @@ int launch_q6k_gemv(const uint8_t *W, const float *x, float *y, int N, int K) {
 // <= 1e-3), more through the f16 MFMA prefill GEMM (q4k_gemm32.hip, <= 1e-2).
 int q6k_gemv(const void *dW, const float *dX, float *dY, int out, int in, int P) {
   if (P > 16) return q6k_gemm32(dW, dX, dY, out, in, P);
+  // 2..16 tokens: one launch of the 32x32 MFMA kernel of q4k_gemv16.hip (FAK_HIP_Q6K_PER_TOKEN=1:
+  // one int8 launch per token, for comparison).
+  if (P > 1 && !env_int("FAK_HIP_Q6K_PER_TOKEN")) return q6k_gemv16(dW, dX, dY, out, in, P);
   for (int t = 0; t < P; ++t)
     if (int rc = launch_q6k_gemv((const uint8_t *)dW, dX + (size_t)t * in, dY + (size_t)t * out,
                                  out, in))
