@@ -96,9 +96,10 @@ def test_graph_begin_needs_a_created_stream(hip):
 
 def test_graph_decode_ffn_replays(hip):
     """A decode step's FFN captured once: the fused MLP (Q4_K down and the q4_k_m Q6_K down, one
-    and three tokens) and Q6_K matmuls (GEMV and prefill GEMM) replay to the bits of the same
-    calls run eagerly, replay after replay, with new activations between replays."""
-    print("[case] graph capture: fused MLP (q4/q6 down), q6k gemv/gemm", flush=True)
+    and three tokens), Q6_K matmuls (GEMV and prefill GEMM) and 8-token verify matmuls (Q4_K and
+    Q6_K: a main launch and an ordered reduce) replay to the bits of the same calls run eagerly,
+    replay after replay, with new activations between replays."""
+    print("[case] graph capture: fused MLP (q4/q6 down), q6k gemv/gemm, 8-token q4k/q6k", flush=True)
     from tests import q6k_cases as qc
     lib = fakhip.load()
     st = C.c_void_p()
@@ -106,7 +107,7 @@ def test_graph_decode_ffn_replays(hip):
     fakhip.call("fhip_set_stream", st)
     allocs, devs = [], []
     try:
-        H, I = 512, 1024
+        H, I = 512, 2048  # K = 2048: the 8-token calls split K in two and reduce
         rng = np.random.default_rng(5)
         q6raw = qc.pin_d(rng.integers(0, 256, H * (I // 256) * 210, dtype=np.uint8), 0x1000)
         g = fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(I, H, 31).ctypes.data, I, H)
@@ -114,10 +115,11 @@ def test_graph_decode_ffn_replays(hip):
         d4 = fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(H, I, 33).ctypes.data, H, I)
         d6 = fakhip.alloc_call("fhip_q6k_upload", q6raw.ctypes.data, H, I)
         allocs += [g, u, d4, d6]
-        x3 = Dev(3 * H * 4)
+        x3 = Dev(8 * H * 4)
         xi = Dev(20 * I * 4)
         devs += [x3, xi]
-        names = [("mlp1", H), ("mlp3", 3 * H), ("mlp6", 3 * H), ("q6gemv", H), ("q6gemm", 20 * H)]
+        names = [("mlp1", H), ("mlp3", 3 * H), ("mlp6", 3 * H), ("q6gemv", H), ("q6gemm", 20 * H),
+                 ("q6v8", 8 * H), ("q4v8", 8 * H)]
         outs = {nm: (Dev(n * 4), Dev(n * 4)) for nm, n in names}
         for a, b in outs.values():
             devs += [a, b]
@@ -128,9 +130,12 @@ def test_graph_decode_ffn_replays(hip):
             fakhip.call("fhip_q4k_mlp_q6down_f32", g, u, d6, x3.ptr, outs["mlp6"][k].ptr, H, I, 3)
             fakhip.call("fhip_q6k_matmul_f32", d6, xi.ptr, outs["q6gemv"][k].ptr, H, I, 1)
             fakhip.call("fhip_q6k_matmul_f32", d6, xi.ptr, outs["q6gemm"][k].ptr, H, I, 20)
+            # verify widths: one main launch + the ordered reduce of the K-range partials
+            fakhip.call("fhip_q6k_matmul_f32", d6, xi.ptr, outs["q6v8"][k].ptr, H, I, 8)
+            fakhip.call("fhip_q4k_matmul_f32", d4, xi.ptr, outs["q4v8"][k].ptr, H, I, 8)
 
         def set_x(seed):
-            fakhip.call("fhip_h2d", x3.ptr, synth.activations(3, H, seed).ctypes.data, 3 * H * 4)
+            fakhip.call("fhip_h2d", x3.ptr, synth.activations(8, H, seed).ctypes.data, 8 * H * 4)
             fakhip.call("fhip_h2d", xi.ptr, synth.activations(20, I, seed + 1).ctypes.data,
                         20 * I * 4)
 
