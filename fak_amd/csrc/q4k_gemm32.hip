@@ -17,8 +17,8 @@
 // as both operands use it: here the K16 slice q holds positions 16q + 8 (lane / 32) + perm8(j),
 // which is where the nibble unpack leaves the weights.
 //
-// For M > 384 Q4_K runs q4k_gemm32s_kernel: the same tile and K order with two waves of 128
-// tokens x 64 rows each and activations staged by direct-to-LDS loads (described there).
+// Q4_K runs q4k_gemm32s_kernel<4>: the same tile and K order with four waves of 128 tokens x
+// 32 rows each and activations staged by direct-to-LDS loads (described there).
 //
 // The same kernel runs Q6_K weights (FMT 1) from the Q6_K tiled records (tiled.hpp): the K16
 // slice q of a row is its 16-weight group q, whose codes sit in one 16-byte ql unit (a nibble)
@@ -371,33 +371,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   } while (0)
 constexpr int wait_vm(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }  // vmcnt(n), lgkmcnt(0)
 
-// Q4_K, M > 384: the staged two-wave form. Same 128-token x 128-row workgroup tile, grid and
-// K order as quant_gemm32_kernel (bit-identical results), but
-//   * each wave owns 128 tokens x 64 rows (4 x 2 MFMA tiles, 128 f32 accumulators), so every
-//     dequantized weight operand feeds four MFMAs instead of two and each weight is dequantized
-//     once per workgroup (the four-wave form dequantizes every row twice);
+// Q4_K: the staged form. Same 128-token x 128-row workgroup tile, grid and K order as
+// quant_gemm32_kernel (bit-identical results), but
+//   * each wave owns all 128 tokens x 128 / NW rows (4 x 4/NW MFMA tiles), so every dequantized
+//     weight operand feeds four MFMAs instead of two and each weight is dequantized once per
+//     workgroup (the four-wave 2x2 form dequantizes every row twice);
 //   * activations go global -> LDS directly (global_load_lds_dwordx4, no staging registers) in
 //     8 KB stages of two K16 slices {h, 2 + h} of a 64-K chunk, four stage buffers, each stage
 //     loaded three stages ahead; every load is issued unconditionally (indices clamped at the
 //     end of K) so each wait is a compile-time count that leaves the later stages in flight;
 //   * the next super-block's records are loaded into registers at the first stage and written to
 //     LDS at the last one, so they get four stages to arrive.
-// Measured at K=3584, N=18944: M=512 101 vs 112 us, M=2048 330 vs 351 us; below M=512 the grid
-// has too few waves for it and the four-wave form is faster.
-__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4k_gemm32s_kernel(
+// NW = 4 (32 rows per wave, 166 VGPRs, 52 KB of LDS: three workgroups, 12 waves per CU) is the
+// default: with 592 workgroups at M=512 on 256 CUs its waves spread to at most three per SIMD
+// (NW = 2 puts two 64-row waves on some SIMDs and one on most). Measured at K=3584, N=18944
+// (us, NW=4 / NW=2 / four-wave 2x2): M=128 44.6 / - / 60.5, M=512 106.5 / 112.7 / 120,
+// M=2048 376 / 413 / 438; the down shape (K=18944, N=3584) at M=512 194 vs 274 (2x2).
+template <int NW>  // waves per workgroup: 2 (64 rows each) or 4 (32 rows each)
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2 ? 2 : 3, NW == 2 ? 2 : 3))) void q4k_gemm32s_kernel(
     const uint8_t *__restrict__ W, const uint4 *__restrict__ xa, float *__restrict__ Y, int N,
     int M, int nblk, int ntiles, int MTG) {
   constexpr int kRec = kQ4kRecord, kUnits = kQ4kRecord / 16;  // 144 units per record
   constexpr int kWU = kBT * kUnits;                             // 1152 units per super-block
-  constexpr int kWPT = kWU / 128;                               // 9 per thread
+  constexpr int kThreads = 64 * NW;
+  constexpr int kWPT = (kWU + kThreads - 1) / kThreads;         // 9 or 5 per thread
   constexpr int kSU = 4 * 2 * 64;                               // 512 units (8 KB) per stage
+  constexpr int NT = 4 / NW;                                    // 32-row MFMA tiles per wave
+  constexpr int kDMA = 8 / NW;                                  // stage loads per wave
   // Four named arrays, not one indexed array: the compiler tracks LDS DMA per object, so a read
   // of one stage does not wait for the DMA into another.
   __shared__ u32x4 As0[kSU];
   __shared__ u32x4 As1[kSU];
   __shared__ u32x4 As2[kSU];
   __shared__ u32x4 As3[kSU];
-  __shared__ u32x4 Ws[kWU];
+  __shared__ u32x4 Ws[kWPT * kThreads];  // past kWU: padding (a repeat of unit 0)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kap = lane >> 5, rho = lane & 31;
@@ -407,19 +414,19 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const u32x4 *xg = reinterpret_cast<const u32x4 *>(xa) + (size_t)(4 * mg) * nq * 64;
   const int tile0 = kBT * ng;
   const u32x4 *Wv = reinterpret_cast<const u32x4 *>(W);
-  auto woff = [&](int k) {  // unit tid + 128 k of the workgroup's 8 records (tile clamped)
-    const int u = tid + 128 * k;
+  auto woff = [&](int k) {  // unit tid + kThreads k of the workgroup's 8 records (tile clamped)
+    const int u = tid + kThreads * k < kWU ? tid + kThreads * k : 0;
     const int rec = u / kUnits, off = u - rec * kUnits;
     const int T = min(tile0 + rec, ntiles - 1);
     return (uint32_t)T * nblk * kUnits + off;
   };
   // Stage s = 8 b + 2 c + h: slices 16 (4 b + c) + h + 2 hi of token tile i at [(2 i + hi) * 64],
-  // one 1 KB wave load each; wave w loads token tiles 2 w and 2 w + 1.
+  // one 1 KB wave load each; wave w loads units kDMA w .. kDMA w + kDMA - 1 (unit 2 i + hi).
   auto load_stage = [&](int s, u32x4 *dst) {
     const int ch = s >> 1, h = s & 1;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = 2 * wave + (j >> 1), hi = j & 1;
+    for (int j = 0; j < kDMA; ++j) {
+      const int p = kDMA * wave + j, i = p >> 1, hi = p & 1;
       __builtin_amdgcn_global_load_lds(
           (const void *)(xg + ((size_t)i * nq + 4 * ch + h + 2 * hi) * 64 + lane),
           (__attribute__((address_space(3))) void *)(dst + (2 * i + hi) * 64), 16, 0, 0);
@@ -427,11 +434,11 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
   auto buf = [&](int k) -> u32x4 * { return k == 0 ? As0 : k == 1 ? As1 : k == 2 ? As2 : As3; };
 
-  f32x16 acc[4][2];
+  f32x16 acc[4][NT];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NT; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
@@ -443,24 +450,26 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   load_stage(1, As1);
   load_stage(2, As2);
 #pragma unroll
-  for (int k = 0; k < kWPT; ++k) Ws[tid + 128 * k] = wreg[k];
+  for (int k = 0; k < kWPT; ++k) Ws[tid + kThreads * k] = wreg[k];
   FHIP_LDS_BARRIER(wait_vm(0));
 
-  const int Tl0 = 4 * wave + (rho >> 4), Tl1 = Tl0 + 2;  // this lane's 16-row tiles
+  // This lane's 16-row tiles: tile t of the wave is local tile (8 / NW) wave + 2 t + rho / 16.
+  auto tl = [&](int t) { return (8 / NW) * wave + 2 * t + (rho >> 4); };
   const int r16 = rho & 15;
   const unsigned char *wbase = reinterpret_cast<const unsigned char *>(Ws);
   for (int b = 0; b < nblk; ++b) {
-    RowScales rs[2];
-    rs[0] = row_scales(__builtin_bit_cast(uint4, *reinterpret_cast<const u32x4 *>(wbase + Tl0 * kRec + 16 * r16)), K);
-    rs[1] = row_scales(__builtin_bit_cast(uint4, *reinterpret_cast<const u32x4 *>(wbase + Tl1 * kRec + 16 * r16)), K);
+    RowScales rs[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      rs[t] = row_scales(__builtin_bit_cast(uint4, *reinterpret_cast<const u32x4 *>(wbase + tl(t) * kRec + 16 * r16)), K);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      uint2 xb[2][2];  // nibble bytes of lane group g = 2 h + kap of chunk c, both row tiles
+      uint2 xb[NT][2];  // nibble bytes of lane group g = 2 h + kap of chunk c, every row tile
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int T = t ? Tl1 : Tl0;
+          const int T = tl(t);
           xb[t][h] = *reinterpret_cast<const uint2 *>(wbase + T * kRec + kQ4kHdr + 1024 * (c >> 1) +
                                                       16 * (16 * (2 * h + kap) + r16) + 8 * (c & 1));
         }
@@ -475,31 +484,31 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           for (int k = 0; k < kWPT; ++k) wreg[k] = Wv[woff(k) + bn * kUnits];
         }
         const u32x4 *Acur = buf(ls & 3);
-        f16x8 bl[2], bh[2];
+        f16x8 bl[NT], bh[NT];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) dequant8(xb[t][h].x, xb[t][h].y, rs[t], c, K, bl[t], bh[t]);
+        for (int t = 0; t < NT; ++t) dequant8(xb[t][h].x, xb[t][h].y, rs[t], c, K, bl[t], bh[t]);
 #pragma unroll
         for (int hi = 0; hi < 2; ++hi) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const f16x8 a = __builtin_bit_cast(f16x8, Acur[(2 * i + hi) * 64 + lane]);
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < NT; ++t)
               acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, hi ? bh[t] : bl[t], acc[i][t], 0, 0, 0);
           }
         }
         if (ls == 7) {
-          FHIP_LDS_BARRIER(wait_vm(63));  // both waves are done reading this super-block's records
+          FHIP_LDS_BARRIER(wait_vm(63));  // every wave is done reading this super-block's records
 #pragma unroll
-          for (int k = 0; k < kWPT; ++k) Ws[tid + 128 * k] = wreg[k];
+          for (int k = 0; k < kWPT; ++k) Ws[tid + kThreads * k] = wreg[k];
         }
         // Stage s + 1 has landed once at most this many of this wave's later loads are pending:
-        // stages s + 2 and s + 3 (4 loads each) and, during stages 0-2, the 9 record loads that
-        // went out after stage s + 1's.
+        // stages s + 2 and s + 3 (kDMA loads each) and, during stages 0-2, the kWPT record
+        // loads that went out after stage s + 1's.
         if (ls <= 2)
-          FHIP_LDS_BARRIER(wait_vm(8 + kWPT));
+          FHIP_LDS_BARRIER(wait_vm(2 * kDMA + kWPT));
         else
-          FHIP_LDS_BARRIER(wait_vm(8));
+          FHIP_LDS_BARRIER(wait_vm(2 * kDMA));
       }
     }
   }
@@ -510,8 +519,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int i = 0; i < 4; ++i) {
     const int t0 = kBM * mg + 32 * i + 4 * kap;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int o = 16 * (kBT * ng + 4 * wave + 2 * t) + rho;
+    for (int t = 0; t < NT; ++t) {
+      const int o = 16 * (kBT * ng + (8 / NW) * wave + 2 * t) + rho;
       if (o >= N) continue;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
@@ -542,10 +551,17 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
   if (fmt == 1) {  // 60 KB of LDS with one weight buffer: two workgroups per CU
     quant_gemm32_kernel<1, 1, 2><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
   } else {
-    // FAK_HIP_GEMM32_FORM: 1 = four-wave kernel, 2 = staged two-wave kernel, else by size.
+    // The staged kernel with four waves of 32 rows, at every M (measured faster than the other
+    // forms from 64 to 2048 tokens). FAK_HIP_GEMM32_FORM: 1 = the four-wave 2x2 kernel, 2 = the
+    // staged kernel with two waves of 64 rows (comparisons; all three agree bit for bit).
     const int form = env_int("FAK_HIP_GEMM32_FORM");
-    if (form == 2 || (form != 1 && MTG >= 4)) {
-      q4k_gemm32s_kernel<<<grid, 128, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
+    if (form == 2) {
+      q4k_gemm32s_kernel<2><<<grid, 128, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
+      FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
+      return FHIP_OK;
+    }
+    if (form != 1) {
+      q4k_gemm32s_kernel<4><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
       FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
       return FHIP_OK;
     }

@@ -104,8 +104,9 @@ def test_q4k_gemm_prefill_7b(hip, oracle_mod, P):
 @pytest.mark.parametrize("out,in_,P", [(300, 768, 600), (1000, 2048, 520), (64, 256, 1000),
                                        (18944, 3584, 512)])
 def test_q4k_gemm_forms_bit_identical(hip, oracle_mod, monkeypatch, out, in_, P):
-    """The staged two-wave GEMM (the default above 384 tokens) and the four-wave GEMM share the
-    tile, the K order and each accumulator's MFMA sequence: their outputs agree bit for bit, on
+    """The staged GEMM (four waves of 32 rows: the default; or two waves of 64 rows) and the
+    four-wave 2x2 GEMM share the tile, the K order and each accumulator's MFMA sequence: their
+    outputs agree bit for bit, on
     whole and ragged row / token tiles, and the staged result meets the GEMM bound against the
     oracle (sampled rows at the 7B shape)."""
     print(f"[case] gemm forms out={out} in={in_} P={P}", flush=True)
@@ -115,8 +116,11 @@ def test_q4k_gemm_forms_bit_identical(hip, oracle_mod, monkeypatch, out, in_, P)
     Y1 = q4k_matmul(raw, out, in_, X, P)
     monkeypatch.setenv("FAK_HIP_GEMM32_FORM", "2")
     Y2 = q4k_matmul(raw, out, in_, X, P)
+    monkeypatch.setenv("FAK_HIP_GEMM32_FORM", "3")
+    Y3 = q4k_matmul(raw, out, in_, X, P)
     monkeypatch.delenv("FAK_HIP_GEMM32_FORM")
     assert np.array_equal(Y1.view(np.uint32), Y2.view(np.uint32))
+    assert np.array_equal(Y1.view(np.uint32), Y3.view(np.uint32))
     if out > 4096:
         rb = (in_ // 256) * 144
         sel = np.concatenate([np.arange(0, 128), np.arange(out - 128, out)])
