@@ -390,7 +390,7 @@ constexpr int wait_vm(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }  /
 template <int NW>  // waves per workgroup: 2 (64 rows each) or 4 (32 rows each)
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2 ? 2 : 3, NW == 2 ? 2 : 3))) void q4k_gemm32s_kernel(
     const uint8_t *__restrict__ W, const uint4 *__restrict__ xa, float *__restrict__ Y, int N,
-    int M, int nblk, int ntiles, int MTG) {
+    int M, int nblk, int ntiles, int MTG, int SK, float *__restrict__ part) {
   constexpr int kRec = kQ4kRecord, kUnits = kQ4kRecord / 16;  // 144 units per record
   constexpr int kWU = kBT * kUnits;                             // 1152 units per super-block
   constexpr int kThreads = 64 * NW;
@@ -408,7 +408,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kap = lane >> 5, rho = lane & 31;
-  const int mg = blockIdx.x % MTG, ng = blockIdx.x / MTG;
+  // Workgroup = (tile, K range sp): SK > 1 splits K for grids too small to fill the GPU; each
+  // range writes its partial sums and a second kernel adds them in range order.
+  const int task = blockIdx.x / SK, sp = blockIdx.x - task * SK;
+  const int mg = task % MTG, ng = task / MTG;
+  const int kb0 = sp * nblk / SK, kb1 = (sp + 1) * nblk / SK;  // >= 1 super-block: SK <= nblk
   const int nq = nblk * 16;
   const Magic K = magic_consts();
   const u32x4 *xg = reinterpret_cast<const u32x4 *>(xa) + (size_t)(4 * mg) * nq * 64;
@@ -423,7 +427,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
   // Stage s = 8 b + 2 c + h: slices 16 (4 b + c) + h + 2 hi of token tile i at [(2 i + hi) * 64],
   // one 1 KB wave load each; wave w loads units kDMA w .. kDMA w + kDMA - 1 (unit 2 i + hi).
   auto load_stage = [&](int s, u32x4 *dst) {
-    const int ch = s >> 1, h = s & 1;
+    const int ch = 4 * kb0 + (s >> 1), h = s & 1;  // s counts from the range start
 #pragma unroll
     for (int j = 0; j < kDMA; ++j) {
       const int p = kDMA * wave + j, i = p >> 1, hi = p & 1;
@@ -442,10 +446,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int nstage = nblk * 8;
+  const int nstage = (kb1 - kb0) * 8;
   u32x4 wreg[kWPT];
 #pragma unroll
-  for (int k = 0; k < kWPT; ++k) wreg[k] = Wv[woff(k)];
+  for (int k = 0; k < kWPT; ++k) wreg[k] = Wv[woff(k) + (uint32_t)kb0 * kUnits];
   load_stage(0, As0);
   load_stage(1, As1);
   load_stage(2, As2);
@@ -457,7 +461,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
   auto tl = [&](int t) { return (8 / NW) * wave + 2 * t + (rho >> 4); };
   const int r16 = rho & 15;
   const unsigned char *wbase = reinterpret_cast<const unsigned char *>(Ws);
-  for (int b = 0; b < nblk; ++b) {
+  for (int b = kb0; b < kb1; ++b) {
     RowScales rs[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -476,10 +480,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int ls = 2 * c + h;  // stage within the super-block (its buffer is ls & 3)
-        const int s = 8 * b + ls;
+        const int s = 8 * (b - kb0) + ls;
         load_stage(min(s + 3, nstage - 1), buf((ls + 3) & 3));
         if (ls == 0) {
-          const uint32_t bn = (uint32_t)min(b + 1, nblk - 1);
+          const uint32_t bn = (uint32_t)min(b + 1, kb1 - 1);
 #pragma unroll
           for (int k = 0; k < kWPT; ++k) wreg[k] = Wv[woff(k) + bn * kUnits];
         }
@@ -525,12 +529,27 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int tok = t0 + 8 * (v >> 2) + (v & 3);
-        if (tok < M) Y[(size_t)tok * N + o] = acc[i][t][v];
+        if (tok >= M) continue;
+        if (SK == 1)
+          Y[(size_t)tok * N + o] = acc[i][t][v];
+        else
+          part[((size_t)sp * M + tok) * N + o] = acc[i][t][v];
       }
     }
   }
 }
 #undef FHIP_LDS_BARRIER
+
+
+// Y = the SK partial results of a K-split GEMM added in range order (deterministic).
+__global__ void gemm32_reduce_kernel(const float *__restrict__ part, float *__restrict__ Y, int SK,
+                                     long long total) {
+  const long long id = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  float v = part[id];
+  for (int s = 1; s < SK; ++s) v += part[(size_t)s * total + id];
+  Y[id] = v;
+}
 
 }  // namespace
 
@@ -539,39 +558,62 @@ size_t gemm32_xa_bytes(int M, int K) { return (size_t)ceil_div(M, kBM) * kBM * K
 namespace {
 int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int K, int M) {
   const int nblk = K / 256;
-  uint4 *xa = (uint4 *)workspace(gemm32_xa_bytes(M, K));
-  if (!xa) return FHIP_ENOMEM;
   const int MTG = ceil_div(M, kBM);
+  const int ntiles = q4k_tiles(N);
+  const int grid = MTG * ceil_div(ntiles, kBT);
+  // FAK_HIP_GEMM32_FORM: 1 = the four-wave 2x2 kernel, 2 = the staged kernel with two waves of
+  // 64 rows (comparisons; all forms agree bit for bit without a K split). Default: the staged
+  // kernel with four waves of 32 rows, measured faster than the others from 64 to 2048 tokens.
+  const int form = fmt == 0 ? env_int("FAK_HIP_GEMM32_FORM") : 1;
+  // K split of the default form when the grid does not fill the GPU (e.g. the 3584-row down
+  // projection, or 128 tokens): about two workgroups per CU, ranges of at least 4 super-blocks;
+  // the partial results are added in range order. FAK_HIP_GEMM32_SK overrides.
+  int SK = 1;
+  if (form != 1 && form != 2) {
+    const int cus = cu_count() > 0 ? cu_count() : 256;
+    SK = env_int("FAK_HIP_GEMM32_SK");
+    if (SK <= 0) SK = grid < cus ? min(ceil_div(2 * cus, grid), nblk / 4) : 1;
+    if (SK < 1) SK = 1;
+    if (SK > nblk) SK = nblk;
+  }
+  const size_t xab = (gemm32_xa_bytes(M, K) + 255) & ~(size_t)255;
+  const size_t pb = SK > 1 ? (size_t)SK * M * N * 4 : 0;
+  unsigned char *ws = (unsigned char *)workspace(xab + pb);
+  if (!ws) return FHIP_ENOMEM;
+  uint4 *xa = (uint4 *)ws;
+  float *part = SK > 1 ? (float *)(ws + xab) : nullptr;
   const long long total = (long long)MTG * 4 * (K / 16) * 64;
   gemm32_xprep_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream()>>>(X, M, K, total, xa);
   FHIP_CHECK_LAUNCH("gemm32_xprep_kernel");
-  const int ntiles = q4k_tiles(N);
-  const int grid = MTG * ceil_div(ntiles, kBT);
   const uint8_t *W = (const uint8_t *)Wv;
   if (fmt == 1) {  // 60 KB of LDS with one weight buffer: two workgroups per CU
     quant_gemm32_kernel<1, 1, 2><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
-  } else {
-    // The staged kernel with four waves of 32 rows, at every M (measured faster than the other
-    // forms from 64 to 2048 tokens). FAK_HIP_GEMM32_FORM: 1 = the four-wave 2x2 kernel, 2 = the
-    // staged kernel with two waves of 64 rows (comparisons; all three agree bit for bit).
-    const int form = env_int("FAK_HIP_GEMM32_FORM");
-    if (form == 2) {
-      q4k_gemm32s_kernel<2><<<grid, 128, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
-      FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
-      return FHIP_OK;
-    }
-    if (form != 1) {
-      q4k_gemm32s_kernel<4><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
-      FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
-      return FHIP_OK;
-    }
-    int nwb = env_int("FAK_HIP_GEMM32_NWB");
-    if (nwb == 0) nwb = 1;
-    if (nwb == 1)
-      quant_gemm32_kernel<0, 1, 3><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
-    else
-      quant_gemm32_kernel<0, 2, 2><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
+    FHIP_CHECK_LAUNCH("quant_gemm32_kernel");
+    return FHIP_OK;
   }
+  if (form == 2) {
+    q4k_gemm32s_kernel<2><<<grid, 128, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG, 1,
+                                                       nullptr);
+    FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
+    return FHIP_OK;
+  }
+  if (form != 1) {
+    q4k_gemm32s_kernel<4><<<grid * SK, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG, SK,
+                                                            part);
+    FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
+    if (SK > 1) {
+      const long long tot = (long long)M * N;
+      gemm32_reduce_kernel<<<(unsigned)((tot + 255) / 256), 256, 0, stream()>>>(part, Y, SK, tot);
+      FHIP_CHECK_LAUNCH("gemm32_reduce_kernel");
+    }
+    return FHIP_OK;
+  }
+  int nwb = env_int("FAK_HIP_GEMM32_NWB");
+  if (nwb == 0) nwb = 1;
+  if (nwb == 1)
+    quant_gemm32_kernel<0, 1, 3><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
+  else
+    quant_gemm32_kernel<0, 2, 2><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
   FHIP_CHECK_LAUNCH("quant_gemm32_kernel");
   return FHIP_OK;
 }

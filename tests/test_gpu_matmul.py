@@ -117,7 +117,9 @@ def test_q4k_gemm_forms_bit_identical(hip, oracle_mod, monkeypatch, out, in_, P)
     monkeypatch.setenv("FAK_HIP_GEMM32_FORM", "2")
     Y2 = q4k_matmul(raw, out, in_, X, P)
     monkeypatch.setenv("FAK_HIP_GEMM32_FORM", "3")
+    monkeypatch.setenv("FAK_HIP_GEMM32_SK", "1")  # no K split: the same summation order
     Y3 = q4k_matmul(raw, out, in_, X, P)
+    monkeypatch.delenv("FAK_HIP_GEMM32_SK")
     monkeypatch.delenv("FAK_HIP_GEMM32_FORM")
     assert np.array_equal(Y1.view(np.uint32), Y2.view(np.uint32))
     assert np.array_equal(Y1.view(np.uint32), Y3.view(np.uint32))
@@ -130,6 +132,29 @@ def test_q4k_gemm_forms_bit_identical(hip, oracle_mod, monkeypatch, out, in_, P)
     else:
         ref = oracle_mod.q4k_gemm(raw, out, in_, X, P, workers=16)
         got = Y2
+    assert rel_err(got, ref) <= GEMM_TOL
+
+
+@pytest.mark.parametrize("out,in_,P", [(3584, 18944, 512), (1000, 2048, 520), (18944, 3584, 128),
+                                       (300, 4096, 40)])
+def test_q4k_gemm_k_split(hip, oracle_mod, out, in_, P):
+    """Grids too small for the GPU split K and add the ranges' partial sums in range order: the
+    result meets the GEMM bound against the oracle (sampled rows for the 7B shapes) and is the
+    same bits call after call."""
+    print(f"[case] gemm k split out={out} in={in_} P={P}", flush=True)
+    raw = synth.q4k_weights(out, in_, seed=out + 7 * P)
+    X = synth.activations(P, in_, seed=P + 11)
+    Y = q4k_matmul(raw, out, in_, X, P)
+    assert np.array_equal(Y.view(np.uint32), q4k_matmul(raw, out, in_, X, P).view(np.uint32))
+    if out * in_ > 4_000_000:
+        rb = (in_ // 256) * 144
+        sel = np.concatenate([np.arange(0, 32), np.arange(out - 32, out)])
+        sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
+        ref = oracle_mod.q4k_gemm(sub, len(sel), in_, X, P, workers=16)
+        got = Y[:, sel]
+    else:
+        ref = oracle_mod.q4k_gemm(raw, out, in_, X, P, workers=16)
+        got = Y
     assert rel_err(got, ref) <= GEMM_TOL
 
 
