@@ -621,8 +621,11 @@ size_t gemv_i8_ws_bytes(int ntiles, int K, int M, bool swiglu) {
 int q4k_gemv(const void *Wv, const float *X, float *Y, int N, int K, int M) {
   if (M < 1 || M > 16) return fail(FHIP_EINVAL, "q4k_gemv: M=%d outside 1..16", M);
   if (env_int("FAK_HIP_GEMV_WIDE")) return q4k_gemv_wide(Wv, X, Y, N, K, M);
-  const int from16 = env_int("FAK_HIP_GEMV16_FROM");  // first width on q4k_gemv16 (default 5)
-  if (M >= (from16 > 1 ? from16 : 5)) return q4k_gemv16(Wv, X, Y, N, K, M);
+  // First width on q4k_gemv16: 5, or 3 for K >= 24576, where the int8 kernel's four-token
+  // workgroups measured 36-37 us on a 5120 x 25600 matrix against 30-32 us (at K = 18944 and at
+  // K = 5120 the int8 kernel stays 20-35% faster). FAK_HIP_GEMV16_FROM overrides.
+  const int from16 = env_int("FAK_HIP_GEMV16_FROM");
+  if (M >= (from16 > 1 ? from16 : K >= 24576 ? 3 : 5)) return q4k_gemv16(Wv, X, Y, N, K, M);
   GemvGroup g = {};
   g.W[0] = (const uint8_t *)Wv;
   g.Y[0] = Y;

@@ -82,7 +82,7 @@ def test_q4k_gemv_split_k_repeatable(hip, monkeypatch):
     assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
 
 
-@pytest.mark.parametrize("P", [1, 4, 8, 16])
+@pytest.mark.parametrize("P", [1, 3, 4, 8, 16])
 @pytest.mark.parametrize("out,in_", [(25600, 5120), (5120, 25600)])
 def test_q4k_small_m_27b(hip, oracle_mod, out, in_, P):
     """Speculative-verify widths on the 27B-class FFN."""
