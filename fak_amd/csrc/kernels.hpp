@@ -38,7 +38,7 @@ struct GemvGroup {
 };
 int q4k_gemv_group(const GemvGroup &g, const float *X, int K, int M);
 int q4k_gemv_wide(const void *W, const float *X, float *Y, int N, int K, int M);
-// 5..16 tokens on the 32x32x16 MFMA with exact weight operands (q4k_gemv16.hip).
+// 5..16 tokens (3..16 for K >= 24576) on the 32x32x16 MFMA with exact weight operands (q4k_gemv16.hip).
 int q4k_gemv16(const void *W, const float *X, float *Y, int N, int K, int M);
 // The same for a tiled Q6_K weight.
 int q6k_gemv16(const void *W, const float *X, float *Y, int N, int K, int M);

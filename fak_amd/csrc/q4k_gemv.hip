@@ -1,5 +1,6 @@
 // q4k_gemv.hip — small-M (1..4 tokens) Q4_K matmul: the decode GEMV run for every generated
-// token, and narrow speculative-verify batches. Wider batches (5..16) use q4k_gemv16.hip.
+// token, and narrow speculative-verify batches. Wider batches (5..16, or 3..16 on rows of
+// K >= 24576) use q4k_gemv16.hip.
 //
 // Computes Y[t][o] = sum_k W[o][k] * X[t][k] with W the dequantized Q4_K weight
 // (w = d*sc_s*n - dmin*m_s for sub-block s, internal/model/quant_q4k.go:90-111) without ever
@@ -615,7 +616,7 @@ size_t gemv_i8_ws_bytes(int ntiles, int K, int M, bool swiglu) {
   return p.xop_bytes + p.part_bytes;
 }
 
-// Small-M entry: 1..4 tokens on the int8 kernel, 5..16 on the 32x32 MFMA kernel of
+// Small-M entry: 1..4 tokens on the int8 kernel, 5..16 (3..16 for K >= 24576) on the 32x32 MFMA kernel of
 // q4k_gemv16.hip (FAK_HIP_GEMV_WIDE=1 forces the older f16 kernel of q4k_gemv_wide.hip for
 // every width).
 int q4k_gemv(const void *Wv, const float *X, float *Y, int N, int K, int M) {
