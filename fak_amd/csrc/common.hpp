@@ -1,5 +1,5 @@
-// common.hpp — shared plumbing of the fakhip C ABI: status codes, the current stream, the
-// grow-only device workspace.
+// common.hpp — shared plumbing of the fakhip C ABI: status codes, the current stream, device
+// scratch, the tuning knobs and the registry of tiled weights.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -21,15 +21,60 @@ int hip_fail(hipError_t e, const char *what);
 // Clear the per-thread error message at the start of an entry point.
 void clear_error();
 
-// Device scratch owned by the library, grown on demand. A grow allocates a new buffer and
-// keeps the old one (queued kernels and captured graphs may still use it). Returns nullptr
-// (and records the error) on failure.
+// Device scratch for the launches of one call, `bytes` long. Normally the current stream's
+// workspace: one grow-only buffer per stream, so work queued on different streams never shares
+// scratch (a grow allocates a new buffer and keeps the old one: queued kernels and captured
+// graphs may still use it). Inside a ScratchScope it is the scope's region instead, and nothing
+// is allocated; a request larger than that region fails. Returns nullptr (and records the
+// error) on failure.
 void *workspace(size_t bytes);
+
+// Routes workspace() to [base, base + cap) until destroyed (scopes nest).
+class ScratchScope {
+ public:
+  ScratchScope(void *base, size_t cap);
+  ~ScratchScope();
+  ScratchScope(const ScratchScope &) = delete;
+  ScratchScope &operator=(const ScratchScope &) = delete;
+
+ private:
+  void *prev_base_;
+  size_t prev_cap_;
+  bool prev_on_;
+};
 
 // Device properties cached by fhip_init.
 int cu_count();
 // Largest dynamic LDS allocation one workgroup may request (bytes).
 int lds_limit();
+
+// Launch-shape overrides, read once from the environment by fhip_init (0 = the built-in rule).
+// None of them changes a result except gemm32_sk, which reorders the GEMM's K-range sums.
+struct Tuning {
+  int gemv_tw, gemv_kw;   // FAK_HIP_GEMV_TW / _KW: 1..4-token GEMV workgroup shape
+  int gemv_globalx;       // FAK_HIP_GEMV_GLOBALX: activation operands in global memory
+  int gemv16_from;        // FAK_HIP_GEMV16_FROM: first width on the 5..16-token kernel (2..5)
+  int gemm32_form;        // FAK_HIP_GEMM32_FORM: 1 = four-wave 2x2, 2 = two-wave staged
+  int gemm32_sk;          // FAK_HIP_GEMM32_SK: K ranges of the prefill GEMM
+  int gemm32_nwb;         // FAK_HIP_GEMM32_NWB: weight buffers of the 2x2 form (1 or 2)
+  int i8r_kw;             // FAK_HIP_I8R_KW: waves per tile of the int8 route
+  int q8_tw, q8_kw;       // FAK_HIP_Q8_TW / _KW: Q8_0 GEMV workgroup shape
+};
+const Tuning &tuning();
+
+// Registry of tiled weights: every repack records the buffer's format and shape, and the matmul
+// entries refuse a pointer that does not start a tiled weight of the format and shape asked for
+// (a raw GGUF upload or a stale pointer would otherwise produce plausible garbage). Any other
+// write through the ABI into a recorded range (copies, memsets, unpack/dequant outputs, frees)
+// drops the record; a device-to-device copy of a whole recorded weight records the copy.
+enum WeightKind { kWeightQ4K = 1, kWeightQ8_0 = 2, kWeightQ6K = 3 };
+void tag_weight(const void *p, size_t bytes, int kind, int out, int in);
+void untag_range(const void *p, size_t bytes);
+int check_weight(const char *who, const void *p, int kind, int out, int in);
+
+// FHIP_EINVAL unless [a, a + na) and [b, b + nb) are disjoint (an input that lives in the
+// scratch a launch is about to overwrite).
+int check_disjoint(const char *who, const void *a, size_t na, const void *b, size_t nb);
 
 }  // namespace fhip
 

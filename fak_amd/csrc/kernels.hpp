@@ -16,16 +16,14 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // every product pairs a weight with its own activation.
 __host__ __device__ constexpr int perm8(int j) { return (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1); }
 
-// Large-M activation operands for the GEMM: X [M][K] f32 -> f16 tiles in MFMA A-operand order:
-//   xa[((mt * (K/32) + s) * 64 + l)] = 8 f16 values f16(x[16 mt + (l & 15)][32 s + 8 (l >> 4)
-//   + perm8(j)]), rows past M are zero. The 16-token tile count is padded to a multiple of
-//   kGemmTilePad so every workgroup's token tiles exist. Bytes: gemm_mt(M) * 16 * K * 2.
-constexpr int kGemmTilePad = 8;
-inline int gemm_mt(int M) { return ceil_div(ceil_div(M, 16), kGemmTilePad) * kGemmTilePad; }
-inline size_t gemm_xa_bytes(int M, int K) { return (size_t)gemm_mt(M) * 16 * K * 2; }
-int launch_gemm_xprep(const float *X, int M, int K, void *xa);
+// A checked Q4_K matmul of P tokens (the route of fhip_q4k_matmul_f32) and the scratch bytes
+// (workspace()) it needs.
+int q4k_matmul_run(const void *W, const float *X, float *Y, int N, int K, int P);
+size_t q4k_matmul_ws_bytes(int N, int K, int P);
 
 int q4k_gemv(const void *W, const float *X, float *Y, int N, int K, int M);
+// Scratch bytes (workspace()) of one q4k_gemv call.
+size_t q4k_gemv_ws_bytes(int N, int K, int M);
 // Matrices sharing one activation, run as one grid (the group dispatch of
 // internal/model/metal_q4k_on.go:139-190). Members are concatenated by 16-row tiles.
 constexpr int kMaxGroup = 8;
@@ -37,21 +35,23 @@ struct GemvGroup {
   int count;
 };
 int q4k_gemv_group(const GemvGroup &g, const float *X, int K, int M);
-int q4k_gemv_wide(const void *W, const float *X, float *Y, int N, int K, int M);
 // 5..16 tokens (3..16 for K >= 24576) on the 32x32x16 MFMA with exact weight operands (q4k_gemv16.hip).
 int q4k_gemv16(const void *W, const float *X, float *Y, int N, int K, int M);
+// Scratch bytes of a q4k_gemv16 (fmt 0) / q6k_gemv16 (fmt 1) call.
+size_t gemv16_ws_bytes(int fmt, int N, int K, int M);
 // The same for a tiled Q6_K weight.
 int q6k_gemv16(const void *W, const float *X, float *Y, int N, int K, int M);
 // Fused decode MLP pieces (1..4 tokens): the workspace a small-M call over `ntiles` tiles
-// needs, the SwiGLU stage over {gate, up}, a GEMV on a caller-provided workspace, and the Q6_K
-// GEMV.
+// needs, the SwiGLU stage over {gate, up}, and the Q6_K GEMV.
 size_t gemv_i8_ws_bytes(int ntiles, int K, int M, bool swiglu);
 int q4k_gemv_swiglu(const void *gate, const void *up, const float *X, float *inter, int I, int K,
                     int M, void *ws);
-int q4k_gemv_ws(const void *W, const float *X, float *Y, int N, int K, int M, void *ws);
 int q6k_gemv(const void *W, const float *X, float *Y, int N, int K, int M);
-int q4k_gemm(const void *W, const float *X, float *Y, int N, int K, int M);
+// Scratch bytes of one q6k_gemv call.
+size_t q6k_gemv_ws_bytes(int N, int K, int M);
 int q4k_gemm32(const void *W, const float *X, float *Y, int N, int K, int M);
+// Scratch bytes of a q4k_gemm32 (fmt 0) / q6k_gemm32 (fmt 1) call.
+size_t gemm32_ws_bytes(int fmt, int N, int K, int M);
 // The same GEMM over a tiled Q6_K weight (prefill of the q4_k_m Q6_K tensors).
 int q6k_gemm32(const void *W, const float *X, float *Y, int N, int K, int M);
 int q8_0_gemv(const void *W, const float *X, float *Y, int N, int K, int M);
@@ -80,8 +80,5 @@ __device__ __forceinline__ uint32_t pack_byte(int a, int b, int c, int d, int k)
 // Workgroup shape of the small-M GEMV kernels (TW tiles x KW waves; see q4k_gemv.hip).
 void gemv_shape(int ntiles, int nblk, int max_waves, size_t lds_fixed, size_t lds_per_wave,
                 int &TW, int &KW);
-
-// Read an integer tuning override from the environment (0 when unset).
-int env_int(const char *name);
 
 }  // namespace fhip

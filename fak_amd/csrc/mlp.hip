@@ -27,25 +27,32 @@ int check_mlp(const char *who, const void *g, const void *u, const void *d, cons
   if (((uintptr_t)g & 15) || ((uintptr_t)u & 15) || ((uintptr_t)dX & 15) ||
       (q4_down && ((uintptr_t)d & 15)))
     return fail(FHIP_EINVAL, "%s: dX and the Q4_K weights must be 16-byte aligned", who);
-  return FHIP_OK;
+  if (P == 0) return FHIP_OK;
+  if (int rc = check_weight(who, g, kWeightQ4K, inter, hidden)) return rc;
+  if (int rc = check_weight(who, u, kWeightQ4K, inter, hidden)) return rc;
+  return check_weight(who, d, q4_down ? kWeightQ4K : kWeightQ6K, hidden, inter);
 }
 
-// Workspace: the intermediate [P][inter] (256-byte padded), then one scratch area shared by
-// the two launches (stream-ordered).
+// Workspace: the intermediate [P][inter] (256-byte padded), then the scratch of the two
+// launches (stream-ordered, so they may share it). The down GEMV is the plain matmul of the
+// intermediate, run inside a ScratchScope over the second region: its own scratch (operands,
+// K-range partials) can never land on the intermediate it reads.
 int run_mlp(const void *g, const void *u, const void *d, const float *dX, float *dY, int hidden,
             int inter, int P, bool q4_down) {
   const size_t interB = ((size_t)P * inter * 4 + 255) & ~(size_t)255;
-  size_t opB = gemv_i8_ws_bytes(2 * q4k_tiles(inter), hidden, P, true);
-  if (q4_down) {
-    const size_t dB = gemv_i8_ws_bytes(q4k_tiles(hidden), inter, P, false);
-    if (dB > opB) opB = dB;
-  }
-  unsigned char *ws = (unsigned char *)workspace(interB + opB + 256);
+  size_t scr = gemv_i8_ws_bytes(2 * q4k_tiles(inter), hidden, P, true);
+  const size_t dB =
+      q4_down ? q4k_gemv_ws_bytes(hidden, inter, P) : q6k_gemv_ws_bytes(hidden, inter, P);
+  if (dB > scr) scr = dB;
+  scr = (scr + 255) & ~(size_t)255;
+  unsigned char *ws = (unsigned char *)workspace(interB + scr);
   if (!ws) return FHIP_ENOMEM;
+  if (int rc = check_disjoint("mlp", dX, (size_t)P * hidden * 4, ws, interB + scr)) return rc;
   float *mid = (float *)ws;
-  void *xop = ws + interB;
-  if (int rc = q4k_gemv_swiglu(g, u, dX, mid, inter, hidden, P, xop)) return rc;
-  if (q4_down) return q4k_gemv_ws(d, mid, dY, hidden, inter, P, xop);
+  unsigned char *rest = ws + interB;
+  ScratchScope scope(rest, scr);
+  if (int rc = q4k_gemv_swiglu(g, u, dX, mid, inter, hidden, P, rest)) return rc;
+  if (q4_down) return q4k_gemv(d, mid, dY, hidden, inter, P);
   return q6k_gemv(d, mid, dY, hidden, inter, P);
 }
 

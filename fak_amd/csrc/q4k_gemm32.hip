@@ -135,29 +135,62 @@ struct GemmFmt {
 };
 
 // Activation operands: xa[(tt * (K/16) + q) * 64 + l] = 8 f16 of token 32 tt + l % 32 at
-// K = 16 q + 8 (l / 32) + perm8(j); token tiles padded to whole workgroups (zeros).
-__global__ void gemm32_xprep_kernel(const float *__restrict__ X, int M, int K, long long total,
-                                    uint4 *__restrict__ xa) {
-  const long long id = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= total) return;
-  const int nq = K / 16;
-  const int l = (int)(id & 63);
-  const long long tq = id >> 6;
-  const int tt = (int)(tq / nq), q = (int)(tq - (long long)tt * nq);
-  const int t = 32 * tt + (l & 31);
-  f16x8 h;
-  if (t < M) {
-    const float *x = X + (size_t)t * K + 16 * q + 8 * (l >> 5);
-    const float4 v0 = *reinterpret_cast<const float4 *>(x);
-    const float4 v1 = *reinterpret_cast<const float4 *>(x + 4);
-    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+// K = 16 q + 8 (l / 32) + perm8(j); token tiles padded to whole workgroups (zeros). Each token
+// row is scaled by a power of two 2^-k that puts its largest magnitude in [2^14, 2^15), so any
+// finite f32 row converts to f16 without overflow and keeps 11-bit relative precision down to
+// 2^-28 of its maximum; the GEMM multiplies the token's outputs by tscale[t] = 2^k (exact), NaN
+// for a row holding a NaN or an infinity (its operands are zeros), 1 for an all-zero row.
+// One workgroup per (padded) token: a max-reduce over the row, then the conversion (the second
+// read of the row hits L2).
+constexpr int kXprepThreads = 256;
+__global__ __launch_bounds__(kXprepThreads) void gemm32_xprep_kernel(
+    const float *__restrict__ X, int M, int K, uint4 *__restrict__ xa, float *__restrict__ tscale) {
+  __shared__ float wmax[kXprepThreads / 64];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const int nq = K / 16, nu = K / 8;  // 16-K slices and 8-value units of the row
+  const bool valid = t < M;
+  const float4 *row = reinterpret_cast<const float4 *>(X + (size_t)(valid ? t : 0) * K);
+  // fmaxf drops NaN: a NaN anywhere must still mark the row, so it is tracked separately.
+  float amax = 0.f;
+  bool bad = false;
+  if (valid)
+    for (int i = tid; i < K / 4; i += kXprepThreads) {
+      const float4 v = row[i];
+      amax = fmaxf(fmaxf(amax, fabsf(v.x)), fmaxf(fmaxf(fabsf(v.y), fabsf(v.z)), fabsf(v.w)));
+      bad |= (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
+    }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) h[j] = (_Float16)v[perm8(j)];
-  } else {
+  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  const bool wbad = __any(bad);
+  if ((tid & 63) == 0) wmax[tid >> 6] = wbad ? __builtin_nanf("") : amax;
+  __syncthreads();
+  float m = 0.f;
+  bool nan = false;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) h[j] = (_Float16)0.f;
+  for (int w = 0; w < kXprepThreads / 64; ++w) {
+    nan |= wmax[w] != wmax[w];
+    m = fmaxf(m, wmax[w]);
   }
-  xa[id] = __builtin_bit_cast(uint4, h);
+  const bool finite = !nan && m <= 3.4028235e38f;
+  int E = 0;
+  (void)frexpf(m, &E);
+  const int k = E - 15;  // m / 2^k in [2^14, 2^15)
+  if (tid == 0) tscale[t] = !finite ? __builtin_nanf("") : m > 0.f ? ldexpf(1.f, k) : 1.f;
+  const int tt = t >> 5, lt = t & 31;
+  for (int u = tid; u < nu; u += kXprepThreads) {
+    const int q = u >> 1, half = u & 1;
+    f16x8 h;
+    if (valid && finite) {
+      const float4 v0 = row[2 * u], v1 = row[2 * u + 1];
+      const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = (_Float16)ldexpf(v[perm8(j)], -k);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = (_Float16)0.f;
+    }
+    xa[((size_t)tt * nq + q) * 64 + 32 * half + lt] = __builtin_bit_cast(uint4, h);
+  }
 }
 
 // FMT: 0 Q4_K, 1 Q6_K. NWB: LDS buffers for the weight records (2: the next super-block loads
@@ -166,6 +199,7 @@ __global__ void gemm32_xprep_kernel(const float *__restrict__ X, int M, int K, l
 template <int FMT, int NWB, int WPE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void quant_gemm32_kernel(const uint8_t *__restrict__ W,
                                                          const uint4 *__restrict__ xa,
+                                                         const float *__restrict__ tscale,
                                                          float *__restrict__ Y, int N, int M,
                                                          int nblk, int ntiles, int MTG) {
   using F = GemmFmt<FMT>;
@@ -351,7 +385,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int tok = t0 + 8 * (v >> 2) + (v & 3);
-        if (tok < M) Y[(size_t)tok * N + o] = acc[i][t][v];
+        if (tok < M) Y[(size_t)tok * N + o] = acc[i][t][v] * tscale[tok];
       }
     }
   }
@@ -389,7 +423,8 @@ constexpr int wait_vm(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }  /
 // M=2048 376 / 413 / 438; the down shape (K=18944, N=3584) at M=512 194 vs 274 (2x2).
 template <int NW>  // waves per workgroup: 2 (64 rows each) or 4 (32 rows each)
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2 ? 2 : 3, NW == 2 ? 2 : 3))) void q4k_gemm32s_kernel(
-    const uint8_t *__restrict__ W, const uint4 *__restrict__ xa, float *__restrict__ Y, int N,
+    const uint8_t *__restrict__ W, const uint4 *__restrict__ xa,
+    const float *__restrict__ tscale, float *__restrict__ Y, int N,
     int M, int nblk, int ntiles, int MTG, int SK, float *__restrict__ part) {
   constexpr int kRec = kQ4kRecord, kUnits = kQ4kRecord / 16;  // 144 units per record
   constexpr int kWU = kBT * kUnits;                             // 1152 units per super-block
@@ -530,10 +565,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
       for (int v = 0; v < 16; ++v) {
         const int tok = t0 + 8 * (v >> 2) + (v & 3);
         if (tok >= M) continue;
+        const float val = acc[i][t][v] * tscale[tok];
         if (SK == 1)
-          Y[(size_t)tok * N + o] = acc[i][t][v];
+          Y[(size_t)tok * N + o] = val;
         else
-          part[((size_t)sp * M + tok) * N + o] = acc[i][t][v];
+          part[((size_t)sp * M + tok) * N + o] = val;
       }
     }
   }
@@ -553,53 +589,69 @@ __global__ void gemm32_reduce_kernel(const float *__restrict__ part, float *__re
 
 }  // namespace
 
-size_t gemm32_xa_bytes(int M, int K) { return (size_t)ceil_div(M, kBM) * kBM * K * 2; }
-
 namespace {
-int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int K, int M) {
+
+// Launch plan of one GEMM call: form, K split and the scratch it needs (activation operands,
+// token scales, then the K-range partial results).
+struct GemmPlan {
+  int MTG, grid, form, SK;
+  size_t xab, tsb, pb;
+};
+
+GemmPlan plan_gemm32(int fmt, int N, int K, int M) {
+  GemmPlan p{};
   const int nblk = K / 256;
-  const int MTG = ceil_div(M, kBM);
-  const int ntiles = q4k_tiles(N);
-  const int grid = MTG * ceil_div(ntiles, kBT);
+  p.MTG = ceil_div(M, kBM);
+  p.grid = p.MTG * ceil_div(q4k_tiles(N), kBT);
   // FAK_HIP_GEMM32_FORM: 1 = the four-wave 2x2 kernel, 2 = the staged kernel with two waves of
   // 64 rows (comparisons; all forms agree bit for bit without a K split). Default: the staged
   // kernel with four waves of 32 rows, measured faster than the others from 64 to 2048 tokens.
-  const int form = fmt == 0 ? env_int("FAK_HIP_GEMM32_FORM") : 1;
+  p.form = fmt == 0 ? tuning().gemm32_form : 1;
   // K split of the default form when the grid does not fill the GPU (e.g. the 3584-row down
   // projection, or 128 tokens): about two workgroups per CU, ranges of at least 4 super-blocks;
   // the partial results are added in range order. FAK_HIP_GEMM32_SK overrides.
-  int SK = 1;
-  if (form != 1 && form != 2) {
+  p.SK = 1;
+  if (p.form != 1 && p.form != 2) {
     const int cus = cu_count() > 0 ? cu_count() : 256;
-    SK = env_int("FAK_HIP_GEMM32_SK");
-    if (SK <= 0) SK = grid < cus ? min(ceil_div(2 * cus, grid), nblk / 4) : 1;
-    if (SK < 1) SK = 1;
-    if (SK > nblk) SK = nblk;
+    p.SK = tuning().gemm32_sk;
+    if (p.SK <= 0) p.SK = p.grid < cus ? min(ceil_div(2 * cus, p.grid), nblk / 4) : 1;
+    if (p.SK < 1) p.SK = 1;
+    if (p.SK > nblk) p.SK = nblk;
   }
-  const size_t xab = (gemm32_xa_bytes(M, K) + 255) & ~(size_t)255;
-  const size_t pb = SK > 1 ? (size_t)SK * M * N * 4 : 0;
-  unsigned char *ws = (unsigned char *)workspace(xab + pb);
+  p.xab = ((size_t)p.MTG * kBM * K * 2 + 255) & ~(size_t)255;
+  p.tsb = ((size_t)p.MTG * kBM * 4 + 255) & ~(size_t)255;
+  p.pb = p.SK > 1 ? (size_t)p.SK * M * N * 4 : 0;
+  return p;
+}
+
+int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int K, int M) {
+  const int nblk = K / 256;
+  const int ntiles = q4k_tiles(N);
+  const GemmPlan p = plan_gemm32(fmt, N, K, M);
+  const int MTG = p.MTG, grid = p.grid, SK = p.SK;
+  unsigned char *ws = (unsigned char *)workspace(p.xab + p.tsb + p.pb);
   if (!ws) return FHIP_ENOMEM;
+  if (int rc = check_disjoint("gemm32", X, (size_t)M * K * 4, ws, p.xab + p.tsb + p.pb)) return rc;
   uint4 *xa = (uint4 *)ws;
-  float *part = SK > 1 ? (float *)(ws + xab) : nullptr;
-  const long long total = (long long)MTG * 4 * (K / 16) * 64;
-  gemm32_xprep_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream()>>>(X, M, K, total, xa);
+  float *ts = (float *)(ws + p.xab);
+  float *part = SK > 1 ? (float *)(ws + p.xab + p.tsb) : nullptr;
+  gemm32_xprep_kernel<<<MTG * kBM, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
   FHIP_CHECK_LAUNCH("gemm32_xprep_kernel");
   const uint8_t *W = (const uint8_t *)Wv;
   if (fmt == 1) {  // 60 KB of LDS with one weight buffer: two workgroups per CU
-    quant_gemm32_kernel<1, 1, 2><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
+    quant_gemm32_kernel<1, 1, 2><<<grid, 256, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles, MTG);
     FHIP_CHECK_LAUNCH("quant_gemm32_kernel");
     return FHIP_OK;
   }
-  if (form == 2) {
-    q4k_gemm32s_kernel<2><<<grid, 128, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG, 1,
+  if (p.form == 2) {
+    q4k_gemm32s_kernel<2><<<grid, 128, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles, MTG, 1,
                                                        nullptr);
     FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
     return FHIP_OK;
   }
-  if (form != 1) {
-    q4k_gemm32s_kernel<4><<<grid * SK, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG, SK,
-                                                            part);
+  if (p.form != 1) {
+    q4k_gemm32s_kernel<4><<<grid * SK, 256, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles, MTG,
+                                                            SK, part);
     FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
     if (SK > 1) {
       const long long tot = (long long)M * N;
@@ -608,16 +660,19 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
     }
     return FHIP_OK;
   }
-  int nwb = env_int("FAK_HIP_GEMM32_NWB");
-  if (nwb == 0) nwb = 1;
-  if (nwb == 1)
-    quant_gemm32_kernel<0, 1, 3><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
+  if (tuning().gemm32_nwb == 2)
+    quant_gemm32_kernel<0, 2, 2><<<grid, 256, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles, MTG);
   else
-    quant_gemm32_kernel<0, 2, 2><<<grid, 256, 0, stream()>>>(W, xa, Y, N, M, nblk, ntiles, MTG);
+    quant_gemm32_kernel<0, 1, 3><<<grid, 256, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles, MTG);
   FHIP_CHECK_LAUNCH("quant_gemm32_kernel");
   return FHIP_OK;
 }
 }  // namespace
+
+size_t gemm32_ws_bytes(int fmt, int N, int K, int M) {
+  const GemmPlan p = plan_gemm32(fmt, N, K, M);
+  return p.xab + p.tsb + p.pb;
+}
 
 int q4k_gemm32(const void *Wv, const float *X, float *Y, int N, int K, int M) {
   return launch_gemm32(0, Wv, X, Y, N, K, M);

@@ -483,8 +483,8 @@ void i8_shape(int ntiles, int nblk, int max_waves, size_t lds_fixed, size_t lds_
               int &TW, int &KW) {
   const int cus = cu_count() > 0 ? cu_count() : 256;
   const size_t lds_max = (size_t)lds_limit();
-  TW = env_int("FAK_HIP_GEMV_TW");
-  KW = env_int("FAK_HIP_GEMV_KW");
+  TW = tuning().gemv_tw;
+  KW = tuning().gemv_kw;
   if (KW <= 0) {
     KW = 1;
     while (2 * KW <= max_waves && nblk >= 6 * 2 * KW) KW *= 2;
@@ -531,12 +531,9 @@ I8Plan plan_i8(int ntiles, int K, bool swiglu) {
   const int nblk = K / 256;
   const int max_waves = MP == 1 ? kMaxWaves1 : 8;
   I8Plan p{};
-  // Split K across workgroups only on request (FAK_HIP_GEMV_SK): measured on the 7B and 27B
-  // down projections it gains at most 5% and loses elsewhere.
-  p.SK = swiglu ? 1 : env_int("FAK_HIP_GEMV_SK");
-  if (p.SK <= 0) p.SK = 1;
-  if (p.SK > nblk) p.SK = nblk;
-  if (p.SK > 1 && ntiles > kMaxSplitTiles) p.SK = 1;
+  // No split of K across workgroups: measured on the 7B and 27B down projections it gained at
+  // most 5% and lost elsewhere.
+  p.SK = 1;
   const int nbp = (nblk + p.SK - 1) / p.SK;  // super-blocks per split (at most)
   const size_t ldsx = (size_t)nbp * op_bytes<MP>();
   i8_shape(ntiles, nblk / p.SK, max_waves, ldsx, (size_t)64 * NT * 4, p.TW, p.KW);
@@ -551,7 +548,7 @@ I8Plan plan_i8(int ntiles, int K, bool swiglu) {
   }
   const size_t redB =
       (size_t)p.TW * p.KW * 64 * NT * 4 + (swiglu ? (size_t)p.TW * 64 * NT * 4 : 0);
-  p.lds_x = !env_int("FAK_HIP_GEMV_GLOBALX") && ldsx + redB <= (size_t)lds_limit();
+  p.lds_x = !tuning().gemv_globalx && ldsx + redB <= (size_t)lds_limit();
   p.lds_bytes = (p.lds_x ? ldsx : 0) + redB;
   p.xop_bytes = p.lds_x ? 0 : (((size_t)nblk * op_bytes<MP>() + 255) & ~(size_t)255);
   p.part_bytes = p.SK > 1 ? (size_t)p.SK * ntiles * 64 * 4 : 0;
@@ -568,6 +565,7 @@ int launch_i8(const GemvGroup &g, const float *X, int K, int M, bool swiglu, voi
   const size_t wsB = p.xop_bytes + p.part_bytes;
   if (!ws && wsB) ws = workspace(wsB);
   if (wsB && !ws) return FHIP_ENOMEM;
+  if (int rc = check_disjoint("q4k_gemv", X, (size_t)M * K * 4, ws, wsB)) return rc;
   unsigned char *xop = (unsigned char *)ws;
   float *part = p.part_bytes ? (float *)((unsigned char *)ws + p.xop_bytes) : nullptr;
   const int grid = ceil_div(ntiles, p.TW) * p.SK, threads = 64 * p.TW * p.KW;
@@ -598,7 +596,16 @@ int launch_i8_any(const GemvGroup &g, const float *X, int K, int M, bool swiglu 
                   void *ws = nullptr) {
   if (M == 1) return launch_i8<1>(g, X, K, M, swiglu, ws);
   if (M == 2) return launch_i8<2>(g, X, K, M, swiglu, ws);
-  return launch_i8<4>(g, X, K, M, swiglu, ws);
+  if (M <= 4) return launch_i8<4>(g, X, K, M, swiglu, ws);
+  return fail(FHIP_EINVAL, "q4k_gemv: the int8 kernel takes 1..4 tokens, not %d", M);
+}
+
+// First width on the 5..16-token kernel: 5, or 3 for K >= 24576, where the int8 kernel's
+// four-token workgroups measured 36-37 us on a 5120 x 25600 matrix against 30-32 us (at K = 18944
+// and at K = 5120 the int8 kernel stays 20-35% faster). FAK_HIP_GEMV16_FROM (2..5) overrides.
+int gemv16_from(int K) {
+  const int f = tuning().gemv16_from;
+  return f ? f : K >= 24576 ? 3 : 5;
 }
 
 }  // namespace
@@ -616,17 +623,17 @@ size_t gemv_i8_ws_bytes(int ntiles, int K, int M, bool swiglu) {
   return p.xop_bytes + p.part_bytes;
 }
 
-// Small-M entry: 1..4 tokens on the int8 kernel, 5..16 (3..16 for K >= 24576) on the 32x32 MFMA kernel of
-// q4k_gemv16.hip (FAK_HIP_GEMV_WIDE=1 forces the older f16 kernel of q4k_gemv_wide.hip for
-// every width).
+// Scratch bytes of a 1..16-token Q4_K matmul of an [N, K] weight (the route q4k_gemv takes).
+size_t q4k_gemv_ws_bytes(int N, int K, int M) {
+  if (M >= gemv16_from(K)) return gemv16_ws_bytes(0, N, K, M);
+  return gemv_i8_ws_bytes(q4k_tiles(N), K, M, false);
+}
+
+// Small-M entry: 1..4 tokens on the int8 kernel, 5..16 (3..16 for K >= 24576) on the 32x32 MFMA
+// kernel of q4k_gemv16.hip.
 int q4k_gemv(const void *Wv, const float *X, float *Y, int N, int K, int M) {
   if (M < 1 || M > 16) return fail(FHIP_EINVAL, "q4k_gemv: M=%d outside 1..16", M);
-  if (env_int("FAK_HIP_GEMV_WIDE")) return q4k_gemv_wide(Wv, X, Y, N, K, M);
-  // First width on q4k_gemv16: 5, or 3 for K >= 24576, where the int8 kernel's four-token
-  // workgroups measured 36-37 us on a 5120 x 25600 matrix against 30-32 us (at K = 18944 and at
-  // K = 5120 the int8 kernel stays 20-35% faster). FAK_HIP_GEMV16_FROM overrides.
-  const int from16 = env_int("FAK_HIP_GEMV16_FROM");
-  if (M >= (from16 > 1 ? from16 : K >= 24576 ? 3 : 5)) return q4k_gemv16(Wv, X, Y, N, K, M);
+  if (M >= gemv16_from(K)) return q4k_gemv16(Wv, X, Y, N, K, M);
   GemvGroup g = {};
   g.W[0] = (const uint8_t *)Wv;
   g.Y[0] = Y;
@@ -641,12 +648,9 @@ int q4k_gemv(const void *Wv, const float *X, float *Y, int N, int K, int M) {
 // tokens; wider batches run the members one after another.
 int q4k_gemv_group(const GemvGroup &g, const float *X, int K, int M) {
   if (M < 1 || M > 16) return fail(FHIP_EINVAL, "q4k_gemv_group: M=%d outside 1..16", M);
-  if (M > 4 || env_int("FAK_HIP_GEMV_WIDE")) {
-    const bool wide = env_int("FAK_HIP_GEMV_WIDE") != 0;
+  if (M > 4) {
     for (int i = 0; i < g.count; ++i)
-      if (int rc = wide ? q4k_gemv_wide(g.W[i], X, g.Y[i], g.N[i], K, M)
-                        : q4k_gemv16(g.W[i], X, g.Y[i], g.N[i], K, M))
-        return rc;
+      if (int rc = q4k_gemv16(g.W[i], X, g.Y[i], g.N[i], K, M)) return rc;
     return FHIP_OK;
   }
   return launch_i8_any(g, X, K, M);
@@ -667,20 +671,6 @@ int q4k_gemv_swiglu(const void *gate, const void *up, const float *X, float *int
   g.tile0[2] = 2 * q4k_tiles(I);
   g.count = 2;
   return launch_i8_any(g, X, K, M, true, ws);
-}
-
-// A 1..4-token GEMV with a caller-provided workspace of gemv_i8_ws_bytes(q4k_tiles(N), K, M,
-// false) bytes.
-int q4k_gemv_ws(const void *W, const float *X, float *Y, int N, int K, int M, void *ws) {
-  if (M < 1 || M > 4) return fail(FHIP_EINVAL, "q4k_gemv_ws: M=%d outside 1..4", M);
-  GemvGroup g = {};
-  g.W[0] = (const uint8_t *)W;
-  g.Y[0] = Y;
-  g.N[0] = N;
-  g.tile0[0] = 0;
-  g.tile0[1] = q4k_tiles(N);
-  g.count = 1;
-  return launch_i8_any(g, X, K, M, false, ws);
 }
 
 }  // namespace fhip

@@ -405,10 +405,9 @@ __global__ void gemv16_reduce_kernel(const float4 *__restrict__ part, float4 *__
 // K ranges per call: ranges of 4 super-blocks when K allows it, else of 4 to 5 (the kernel
 // works in passes of two super-blocks, so an odd range pads one; measured at the 7B / 27B FFN
 // shapes at 16 tokens, longer ranges lose parallelism and shorter ones pay more per-range start
-// and partial-sum traffic). FAK_HIP_GEMV16_SK overrides (tuning).
+// and partial-sum traffic).
 int gemv16_splits(int nblk) {
-  int sk = env_int("FAK_HIP_GEMV16_SK");
-  if (sk <= 0) sk = nblk % 4 == 0 ? nblk / 4 : (int)(nblk / 4.6);
+  int sk = nblk % 4 == 0 ? nblk / 4 : (int)(nblk / 4.6);
   if (sk < 1) sk = 1;
   if (sk > nblk) sk = nblk;
   return sk;
@@ -425,6 +424,8 @@ int launch_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M)
   if (SK > 1) {
     part = (float *)workspace((size_t)SK * M * N * 4);
     if (!part) return FHIP_ENOMEM;
+    if (int rc = check_disjoint("gemv16", X, (size_t)M * K * 4, part, (size_t)SK * M * N * 4))
+      return rc;
   }
   quant_gemv16_kernel<FMT><<<nrb * SK, 256, 0, stream()>>>((const uint8_t *)Wv, X, Y, part, N, K,
                                                             M, nblk, ntiles, SK);
@@ -441,6 +442,12 @@ int launch_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M)
   return FHIP_OK;
 }
 }  // namespace
+
+size_t gemv16_ws_bytes(int fmt, int N, int K, int M) {
+  (void)fmt;
+  const int SK = gemv16_splits(K / 256);
+  return SK > 1 ? (size_t)SK * M * N * 4 : 0;
+}
 
 int q4k_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
   return launch_gemv16<0>(Wv, X, Y, N, K, M);

@@ -308,6 +308,7 @@ extern "C" int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, fl
   if (!dPacked || !dX || !dY) return fail(FHIP_EINVAL, "fhip_q4k_matmul_int8_f32: null pointer");
   if (((uintptr_t)dX & 15) != 0)
     return fail(FHIP_EINVAL, "fhip_q4k_matmul_int8_f32: dX must be 16-byte aligned");
+  if (int rc = check_weight("fhip_q4k_matmul_int8_f32", dPacked, kWeightQ4K, out, in)) return rc;
   const int nblk = in / 256;
   const bool fused = P <= kFusedTokens;
   int8_t *qx = nullptr;
@@ -316,6 +317,9 @@ extern "C" int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, fl
     const size_t qbytes = ((size_t)P * in + 255) & ~(size_t)255;
     unsigned char *ws = (unsigned char *)workspace(qbytes + (size_t)P * (in / 32) * sizeof(float2));
     if (!ws) return FHIP_ENOMEM;
+    if (int rc = check_disjoint("fhip_q4k_matmul_int8_f32", dX, (size_t)P * in * 4, ws,
+                                qbytes + (size_t)P * (in / 32) * sizeof(float2)))
+      return rc;
     qx = reinterpret_cast<int8_t *>(ws);
     sdg = reinterpret_cast<float2 *>(ws + qbytes);
     const long long nq = (long long)P * (in / 32);
@@ -328,7 +332,7 @@ extern "C" int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, fl
   const int ntiles = q4k_tiles(out);
   const int groups = ceil_div(P, kTokGroup);
   const int pg = P < kTokGroup ? P : kTokGroup;
-  int KW = env_int("FAK_HIP_I8R_KW");
+  int KW = tuning().i8r_kw;
   if (KW <= 0) {
     KW = 1;
     while (KW < 8 && (long long)ntiles * groups * KW < 16LL * cu_count() && nblk >= 2 * KW)

@@ -123,9 +123,11 @@ int fhip_q4k_repack(void *dPacked, const uint8_t *dRaw, int out, int in) {
   const int nblk = in / 256;
   const long long units = (long long)q4k_tiles(out) * nblk * 144;
   const int bs = 256;
+  untag_range(dPacked, q4k_packed_bytes(out, in));
   q4k_repack_kernel<<<(unsigned)((units + bs - 1) / bs), bs, 0, stream()>>>(
       (uint8_t *)dPacked, dRaw, out, nblk, units);
   FHIP_CHECK_LAUNCH("q4k_repack_kernel");
+  tag_weight(dPacked, q4k_packed_bytes(out, in), kWeightQ4K, out, in);
   return FHIP_OK;
 }
 
@@ -133,6 +135,8 @@ int fhip_q4k_unpack(uint8_t *dRaw, const void *dPacked, int out, int in) {
   clear_error();
   if (int rc = check_q4k_shape("fhip_q4k_unpack", out, in)) return rc;
   if (!dPacked || !dRaw) return fail(FHIP_EINVAL, "fhip_q4k_unpack: null pointer");
+  if (int rc = check_weight("fhip_q4k_unpack", dPacked, kWeightQ4K, out, in)) return rc;
+  untag_range(dRaw, (size_t)out * (in / 256) * kQ4kBlock);
   const int nblk = in / 256;
   const long long units = (long long)q4k_tiles(out) * nblk * 144;
   const int bs = 256;
@@ -146,6 +150,8 @@ int fhip_q4k_dequant_f32(float *dW, const void *dPacked, int out, int in) {
   clear_error();
   if (int rc = check_q4k_shape("fhip_q4k_dequant_f32", out, in)) return rc;
   if (!dPacked || !dW) return fail(FHIP_EINVAL, "fhip_q4k_dequant_f32: null pointer");
+  if (int rc = check_weight("fhip_q4k_dequant_f32", dPacked, kWeightQ4K, out, in)) return rc;
+  untag_range(dW, (size_t)out * in * 4);
   const int nblk = in / 256;
   const long long items = (long long)out * nblk * 8;
   const int bs = 256;

@@ -301,13 +301,29 @@ int check_q6k_shape(const char *who, int out, int in) {
   return FHIP_OK;
 }
 
+// Workgroup shape of the one-token GEMV and whether its activation operands fit in LDS.
+struct Q6Plan {
+  int TW, KW;
+  size_t ldsx, redB;
+  bool lds_x;
+};
+
+Q6Plan plan_q6k(int N, int K) {
+  Q6Plan p{};
+  const int nblk = K / 256, ntiles = q4k_tiles(N);
+  p.ldsx = (size_t)nblk * kQ6Op;
+  gemv_shape(ntiles, nblk, 8, p.ldsx, 64 * 4, p.TW, p.KW);
+  p.redB = (size_t)p.TW * p.KW * 64 * 4;
+  p.lds_x = p.ldsx + p.redB <= (size_t)lds_limit();
+  return p;
+}
+
 int launch_q6k_gemv(const uint8_t *W, const float *x, float *y, int N, int K) {
   const int nblk = K / 256, ntiles = q4k_tiles(N);
-  const size_t ldsx = (size_t)nblk * kQ6Op;
-  int TW, KW;
-  gemv_shape(ntiles, nblk, 8, ldsx, 64 * 4, TW, KW);
-  const size_t redB = (size_t)TW * KW * 64 * 4;
-  const bool lds_x = ldsx + redB <= (size_t)lds_limit();
+  const Q6Plan p = plan_q6k(N, K);
+  const int TW = p.TW, KW = p.KW;
+  const size_t ldsx = p.ldsx, redB = p.redB;
+  const bool lds_x = p.lds_x;
   const int grid = ceil_div(ntiles, TW), threads = 64 * TW * KW;
   if (lds_x) {
     q6k_gemv_kernel<true><<<grid, threads, ldsx + redB, stream()>>>(W, x, nullptr, y, N, nblk,
@@ -315,6 +331,7 @@ int launch_q6k_gemv(const uint8_t *W, const float *x, float *y, int N, int K) {
   } else {
     unsigned char *ops = (unsigned char *)workspace(ldsx);
     if (!ops) return FHIP_ENOMEM;
+    if (int rc = check_disjoint("q6k_gemv", x, (size_t)K * 4, ops, ldsx)) return rc;
     q6k_xprep_kernel<<<ceil_div(nblk * 16, 128), 128, 0, stream()>>>(x, nblk, ops);
     FHIP_CHECK_LAUNCH("q6k_xprep_kernel");
     q6k_gemv_kernel<false><<<grid, threads, redB, stream()>>>(W, x, ops, y, N, nblk, TW, KW);
@@ -325,18 +342,20 @@ int launch_q6k_gemv(const uint8_t *W, const float *x, float *y, int N, int K) {
 
 }  // namespace
 
-// Q6_K matmul on the tiled layout: up to 16 tokens one GEMV launch per token (max|dY|/RMS
-// <= 1e-3), more through the f16 MFMA prefill GEMM (q4k_gemm32.hip, <= 1e-2).
+// Q6_K matmul on the tiled layout: one token on the int8 GEMV above, 2..16 tokens in one launch
+// of the 32x32 MFMA kernel of q4k_gemv16.hip (max|dY|/RMS <= 1e-3), more through the f16 MFMA
+// prefill GEMM (q4k_gemm32.hip, <= 1e-2).
+size_t q6k_gemv_ws_bytes(int N, int K, int M) {
+  if (M > 16) return gemm32_ws_bytes(1, N, K, M);
+  if (M > 1) return gemv16_ws_bytes(1, N, K, M);
+  const Q6Plan p = plan_q6k(N, K);
+  return p.lds_x ? 0 : p.ldsx;
+}
+
 int q6k_gemv(const void *dW, const float *dX, float *dY, int out, int in, int P) {
   if (P > 16) return q6k_gemm32(dW, dX, dY, out, in, P);
-  // 2..16 tokens: one launch of the 32x32 MFMA kernel of q4k_gemv16.hip (FAK_HIP_Q6K_PER_TOKEN=1:
-  // one int8 launch per token, for comparison).
-  if (P > 1 && !env_int("FAK_HIP_Q6K_PER_TOKEN")) return q6k_gemv16(dW, dX, dY, out, in, P);
-  for (int t = 0; t < P; ++t)
-    if (int rc = launch_q6k_gemv((const uint8_t *)dW, dX + (size_t)t * in, dY + (size_t)t * out,
-                                 out, in))
-      return rc;
-  return FHIP_OK;
+  if (P > 1) return q6k_gemv16(dW, dX, dY, out, in, P);
+  return launch_q6k_gemv((const uint8_t *)dW, dX, dY, out, in);
 }
 
 }  // namespace fhip
@@ -361,9 +380,11 @@ int fhip_q6k_repack(void *dPacked, const uint8_t *dRaw, int out, int in) {
   if (!dPacked || !dRaw) return fail(FHIP_EINVAL, "fhip_q6k_repack: null pointer");
   const int nblk = in / 256;
   const long long units = (long long)q4k_tiles(out) * nblk * (kQ6kRecord / 16);
+  untag_range(dPacked, q6k_packed_bytes(out, in));
   q6k_repack_kernel<<<(unsigned)((units + 255) / 256), 256, 0, stream()>>>(
       (uint8_t *)dPacked, dRaw, out, nblk, units);
   FHIP_CHECK_LAUNCH("q6k_repack_kernel");
+  tag_weight(dPacked, q6k_packed_bytes(out, in), kWeightQ6K, out, in);
   return FHIP_OK;
 }
 
@@ -371,6 +392,8 @@ int fhip_q6k_unpack(uint8_t *dRaw, const void *dPacked, int out, int in) {
   clear_error();
   if (int rc = check_q6k_shape("fhip_q6k_unpack", out, in)) return rc;
   if (!dPacked || !dRaw) return fail(FHIP_EINVAL, "fhip_q6k_unpack: null pointer");
+  if (int rc = check_weight("fhip_q6k_unpack", dPacked, kWeightQ6K, out, in)) return rc;
+  untag_range(dRaw, fhip_q6k_bytes(out, in));
   const int nblk = in / 256;
   const long long bytes = (long long)out * nblk * kQ6kBlock;
   q6k_unpack_kernel<<<(unsigned)((bytes + 255) / 256), 256, 0, stream()>>>(
@@ -406,6 +429,8 @@ int fhip_q6k_dequant_f32(float *dW, const void *dPacked, int out, int in) {
   clear_error();
   if (int rc = check_q6k_shape("fhip_q6k_dequant_f32", out, in)) return rc;
   if (!dPacked || !dW) return fail(FHIP_EINVAL, "fhip_q6k_dequant_f32: null pointer");
+  if (int rc = check_weight("fhip_q6k_dequant_f32", dPacked, kWeightQ6K, out, in)) return rc;
+  untag_range(dW, (size_t)out * in * 4);
   const int nblk = in / 256;
   const long long n = (long long)out * nblk;
   q6k_dequant_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream()>>>(
@@ -422,6 +447,7 @@ int fhip_q6k_matmul_f32(const void *dPacked, const float *dX, float *dY, int out
   if (!dPacked || !dX || !dY) return fail(FHIP_EINVAL, "fhip_q6k_matmul_f32: null pointer");
   if (((uintptr_t)dX & 15) || ((uintptr_t)dPacked & 15))
     return fail(FHIP_EINVAL, "fhip_q6k_matmul_f32: dX and dPacked must be 16-byte aligned");
+  if (int rc = check_weight("fhip_q6k_matmul_f32", dPacked, kWeightQ6K, out, in)) return rc;
   return q6k_gemv(dPacked, dX, dY, out, in, P);
 }
 

@@ -5,9 +5,10 @@
 // with q8_0DequantBlock, internal/model/quant_iquant.go:14-19).
 //
 // Each 32-weight block is one K=32 f16 MFMA step: the codes become exact f16 values through
-// the exponent trick ((b ^ 0x80) | 0x6400 = 1152 + b), the activation is the hi/lo f16 pair of
-// the GEMV (xprep.hip), and after the MFMA the block scale is applied on the VALU:
-//   y += d * (T - 1152 * S),   T = MFMA sum, S = sum of the block's activations.
+// the exponent trick ((b ^ 0x80) | 0x6400 = 1152 + b), the activation is the scaled hi/lo f16
+// pair of gemv_common.hpp (x = e * (hi + lo), e a power of two per block and token), and after
+// the MFMA the block scales are applied on the VALU:
+//   y += (d e) * (T - 1152 * S),   T = MFMA sum, S = sum of the block's scaled activations.
 #include "gemv_common.hpp"
 
 namespace fhip {
@@ -151,14 +152,14 @@ __global__ __launch_bounds__((LX && M <= 8) ? 1024 : 512) void q8_gemv_kernel(
   const int ns = 2 * npairs, nsv = K / 32;  // staged slices (a padded last block stays zero)
   const uint8_t *base = W + (size_t)(tvalid ? T : 0) * npairs * kQ8Record;
   const uint4 *A;
-  const float *Sx;
+  const float2 *Ex;
   if (LX) {
     A = reinterpret_cast<const uint4 *>(smem);
-    Sx = reinterpret_cast<const float *>(smem + xop_a_bytes(M, ns));
+    Ex = reinterpret_cast<const float2 *>(smem + xop_a_bytes(M, ns));
   } else {
     A = xg;
-    Sx = reinterpret_cast<const float *>(reinterpret_cast<const unsigned char *>(xg) +
-                                         xop_a_bytes(M, ns));
+    Ex = reinterpret_cast<const float2 *>(reinterpret_cast<const unsigned char *>(xg) +
+                                          xop_a_bytes(M, ns));
   }
   float *red = reinterpret_cast<float *>(smem + (LX ? xop_bytes(M, ns) : 0));
 
@@ -171,7 +172,7 @@ __global__ __launch_bounds__((LX && M <= 8) ? 1024 : 512) void q8_gemv_kernel(
   }
   if (LX) {
     stage_x<M>(X, K, 0, ns, nsv, reinterpret_cast<uint4 *>(smem),
-               reinterpret_cast<float *>(smem + xop_a_bytes(M, ns)), threadIdx.x, blockDim.x);
+               reinterpret_cast<float2 *>(smem + xop_a_bytes(M, ns)), threadIdx.x, blockDim.x);
     __syncthreads();
   }
 
@@ -197,6 +198,7 @@ __global__ __launch_bounds__((LX && M <= 8) ? 1024 : 512) void q8_gemv_kernel(
       const f16x8 bw =
           __builtin_bit_cast(f16x8, u32x4{b02(x0), b02(x0 >> 8), b02(x1), b02(x1 >> 8)});
       const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hc >> (16 * h)));
+      const bool sv = LX || sl < nsv;
 #pragma unroll
       for (int k = 0; k < NSET; ++k) {
         const int rho = r + 16 * k;
@@ -207,8 +209,9 @@ __global__ __launch_bounds__((LX && M <= 8) ? 1024 : 512) void q8_gemv_kernel(
 #pragma unroll
         for (int jj = 0; jj < J; ++jj) {
           const int t = 8 * k + 2 * g + jj;
-          const float S = (t < M && (LX || sl < nsv)) ? Sx[(sl >> 3) * M * 8 + t * 8 + (sl & 7)] : 0.f;
-          acc[k][jj] = fmaf(d, fmaf(-1152.f, S, dd[2 * jj] + dd[2 * jj + 1]), acc[k][jj]);
+          const float2 se = (t < M && sv) ? Ex[(sl >> 3) * M * 8 + t * 8 + (sl & 7)]
+                                          : make_float2(0.f, 0.f);
+          acc[k][jj] = fmaf(d * se.y, fmaf(-1152.f, se.x, dd[2 * jj] + dd[2 * jj + 1]), acc[k][jj]);
         }
       }
     }
@@ -231,15 +234,32 @@ __global__ __launch_bounds__((LX && M <= 8) ? 1024 : 512) void q8_gemv_kernel(
     }
 }
 
+// Global-path operand writer: one thread per (slice, token); slices >= nsv are zero.
+template <int M>
+__global__ void q8_xprep_kernel(const float *__restrict__ X, int K, int ns, int nsv,
+                                uint4 *__restrict__ A) {
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= ns * M) return;
+  const int t = id / ns, sl = id - t * ns;
+  float2 *E = reinterpret_cast<float2 *>(reinterpret_cast<unsigned char *>(A) + xop_a_bytes(M, ns));
+  split_slice<M>(X + (size_t)t * K + 32 * (sl < nsv ? sl : 0), sl < nsv, sl, t, A, E);
+}
+
+template <int M>
+bool q8_lds_x(int K) {
+  constexpr int VALS = ((2 * M + 15) / 16) * (M < 2 ? M : 2);
+  const size_t stage = xop_bytes(M, 2 * q8_groups(K));
+  return !tuning().gemv_globalx && stage + (size_t)16 * 64 * VALS * 4 <= (size_t)lds_limit();
+}
+
 template <int M>
 int launch_q8(const uint8_t *W, const float *X, float *Y, int N, int K) {
   const int npairs = q8_groups(K), ntiles = q4k_tiles(N), ns = 2 * npairs;
   constexpr int VALS = ((2 * M + 15) / 16) * (M < 2 ? M : 2);
   const size_t stage = xop_bytes(M, ns);
-  const bool lds_x = !env_int("FAK_HIP_GEMV_GLOBALX") &&
-                     stage + (size_t)16 * 64 * VALS * 4 <= (size_t)lds_limit();
+  const bool lds_x = q8_lds_x<M>(K);
   const int max_waves = (lds_x && M <= 8) ? 16 : 8;
-  int TW = env_int("FAK_HIP_Q8_TW"), KW = env_int("FAK_HIP_Q8_KW");
+  int TW = tuning().q8_tw, KW = tuning().q8_kw;
   if (KW <= 0) {
     const int want_waves = 8 * (cu_count() > 0 ? cu_count() : 256);
     KW = 1;
@@ -260,7 +280,10 @@ int launch_q8(const uint8_t *W, const float *X, float *Y, int N, int K) {
   }
   void *xop = workspace(stage);
   if (!xop) return FHIP_ENOMEM;
-  if (int rc = launch_gemv_xprep(X, M, K, ns, xop)) return rc;
+  if (int rc = check_disjoint("q8_0_gemv", X, (size_t)M * K * 4, xop, stage)) return rc;
+  q8_xprep_kernel<M><<<ceil_div(ns * M, 128), 128, 0, stream()>>>(X, K, ns, K / 32,
+                                                                   (uint4 *)xop);
+  FHIP_CHECK_LAUNCH("q8_xprep_kernel");
   q8_gemv_kernel<M, false><<<grid, threads, redB, stream()>>>(W, X, (const uint4 *)xop, Y, N, K,
                                                               npairs, ntiles, TW, KW);
   FHIP_CHECK_LAUNCH("q8_gemv_kernel<global>");
@@ -307,9 +330,11 @@ int fhip_q8_0_repack(void *dPacked, const uint8_t *dRaw, int out, int in) {
   if (!dPacked || !dRaw) return fail(FHIP_EINVAL, "fhip_q8_0_repack: null pointer");
   const int nb = in / 32, npairs = q8_groups(in);
   const long long units = (long long)q4k_tiles(out) * npairs * kUnits;
+  untag_range(dPacked, q8_packed_bytes(out, in));
   q8_repack_kernel<<<(unsigned)((units + 255) / 256), 256, 0, stream()>>>(
       (uint8_t *)dPacked, dRaw, out, nb, npairs, units);
   FHIP_CHECK_LAUNCH("q8_repack_kernel");
+  tag_weight(dPacked, q8_packed_bytes(out, in), kWeightQ8_0, out, in);
   return FHIP_OK;
 }
 
@@ -317,6 +342,8 @@ int fhip_q8_0_unpack(uint8_t *dRaw, const void *dPacked, int out, int in) {
   clear_error();
   if (int rc = check_q8_shape("fhip_q8_0_unpack", out, in)) return rc;
   if (!dPacked || !dRaw) return fail(FHIP_EINVAL, "fhip_q8_0_unpack: null pointer");
+  if (int rc = check_weight("fhip_q8_0_unpack", dPacked, kWeightQ8_0, out, in)) return rc;
+  untag_range(dRaw, (size_t)out * (in / 32) * kQ8Block);
   const int nb = in / 32, npairs = q8_groups(in);
   const long long units = (long long)q4k_tiles(out) * npairs * kUnits;
   q8_unpack_kernel<<<(unsigned)((units + 255) / 256), 256, 0, stream()>>>(
@@ -329,6 +356,8 @@ int fhip_q8_0_dequant_f32(float *dW, const void *dPacked, int out, int in) {
   clear_error();
   if (int rc = check_q8_shape("fhip_q8_0_dequant_f32", out, in)) return rc;
   if (!dPacked || !dW) return fail(FHIP_EINVAL, "fhip_q8_0_dequant_f32: null pointer");
+  if (int rc = check_weight("fhip_q8_0_dequant_f32", dPacked, kWeightQ8_0, out, in)) return rc;
+  untag_range(dW, (size_t)out * in * 4);
   const int nb = in / 32, npairs = q8_groups(in);
   const long long items = (long long)out * nb;
   q8_dequant_kernel<<<(unsigned)((items + 255) / 256), 256, 0, stream()>>>(
@@ -366,6 +395,7 @@ int fhip_q8_0_matmul_f32(const void *dPacked, const float *dX, float *dY, int ou
   if (!dPacked || !dX || !dY) return fail(FHIP_EINVAL, "fhip_q8_0_matmul_f32: null pointer");
   if (((uintptr_t)dX & 15) || ((uintptr_t)dPacked & 15))
     return fail(FHIP_EINVAL, "fhip_q8_0_matmul_f32: dX and dPacked must be 16-byte aligned");
+  if (int rc = check_weight("fhip_q8_0_matmul_f32", dPacked, kWeightQ8_0, out, in)) return rc;
   // The raw-GGUF Q8_0 path is a decode GEMV in the reference; longer batches run in 16-token
   // slices of the same kernel.
   for (int t0 = 0; t0 < P; t0 += 16) {

@@ -1,5 +1,6 @@
-// runtime.hip — device selection, pooled device memory, copies, streams, events and the
-// library-owned workspace of the fakhip C ABI (include/fakhip.h).
+// runtime.hip — device selection, pooled device memory, copies, streams, events, the per-stream
+// workspaces, the tuning knobs and the registry of tiled weights of the fakhip C ABI
+// (include/fakhip.h).
 //
 // The pool mirrors the CUDA tenant's size-bucketed free lists (internal/compute/cuda_kernels.cu:
 // 42-44,108-173): fhip_free parks a block under its bucket size and the next fhip_malloc of the
@@ -7,6 +8,7 @@
 // state.
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -23,15 +25,32 @@ hipStream_t g_stream = nullptr;
 int g_inited = 0;
 int g_cus = 0;
 int g_lds = 64 * 1024;
+Tuning g_tuning = {};
 
 std::mutex g_pool_mu;
 std::unordered_map<void *, size_t> g_live;  // ptr -> bucket bytes
 std::multimap<size_t, void *> g_free;       // bucket bytes -> parked ptr
 size_t g_free_bytes = 0;
 
-void *g_ws = nullptr;
-size_t g_ws_bytes = 0;
-std::vector<void *> g_ws_retired;  // earlier, smaller workspaces (kept for captured graphs)
+// One grow-only workspace per stream. Buffers outgrown (or left by a destroyed stream) are
+// retired, not freed: graphs captured earlier may still launch kernels that use them.
+struct StreamWs {
+  void *buf = nullptr;
+  size_t bytes = 0;
+};
+std::unordered_map<hipStream_t, StreamWs> g_ws;
+std::vector<void *> g_ws_retired;
+
+// The active ScratchScope, if any.
+void *g_scope_base = nullptr;
+size_t g_scope_cap = 0;
+bool g_scope_on = false;
+
+struct Tag {
+  uintptr_t end;
+  int kind, out, in;
+};
+std::map<uintptr_t, Tag> g_tags;  // start -> tiled weight (guarded by g_pool_mu)
 
 size_t bucket(size_t n) {
   if (n <= 4096) return 4096;
@@ -39,11 +58,32 @@ size_t bucket(size_t n) {
   return (n + (2u << 20) - 1) & ~size_t((2u << 20) - 1);
 }
 
+int env_knob(const char *name) {
+  const char *v = getenv(name);
+  return v ? atoi(v) : 0;
+}
+
+const char *kind_name(int k) {
+  return k == kWeightQ4K ? "Q4_K" : k == kWeightQ8_0 ? "Q8_0" : k == kWeightQ6K ? "Q6_K" : "?";
+}
+
+// Drop every record overlapping [a, b) (g_pool_mu held).
+void untag_locked(uintptr_t a, uintptr_t b) {
+  if (a >= b) return;
+  auto it = g_tags.upper_bound(a);
+  if (it != g_tags.begin()) {
+    auto prev = std::prev(it);
+    if (prev->second.end > a) it = prev;
+  }
+  while (it != g_tags.end() && it->first < b) it = g_tags.erase(it);
+}
+
 }  // namespace
 
 hipStream_t stream() { return g_stream; }
 int cu_count() { return g_cus; }
 int lds_limit() { return g_lds; }
+const Tuning &tuning() { return g_tuning; }
 
 void clear_error() { g_err[0] = 0; }
 
@@ -61,19 +101,70 @@ int hip_fail(hipError_t e, const char *what) {
 }
 
 void *workspace(size_t bytes) {
-  if (bytes <= g_ws_bytes) return g_ws;
+  if (g_scope_on) {
+    if (bytes <= g_scope_cap) return g_scope_base;
+    fail(FHIP_EINVAL, "scratch: the call needs %zu bytes, more than the %zu-byte region it was given",
+         bytes, g_scope_cap);
+    return nullptr;
+  }
+  StreamWs &w = g_ws[g_stream];
+  if (bytes <= w.bytes) return w.buf;
   size_t want = bytes + bytes / 4;
   if (want < (16u << 20)) want = 16u << 20;
-  // A smaller workspace is retired, not freed: graphs captured earlier may still launch
-  // kernels that use it (the growth is geometric, so the retired total stays below the
-  // current size).
   void *p = nullptr;
   hipError_t e = hipMalloc(&p, want);
   if (e != hipSuccess) { hip_fail(e, "workspace: hipMalloc"); return nullptr; }
-  if (g_ws) g_ws_retired.push_back(g_ws);
-  g_ws = p;
-  g_ws_bytes = want;
-  return g_ws;
+  if (w.buf) g_ws_retired.push_back(w.buf);
+  w.buf = p;
+  w.bytes = want;
+  return w.buf;
+}
+
+ScratchScope::ScratchScope(void *base, size_t cap)
+    : prev_base_(g_scope_base), prev_cap_(g_scope_cap), prev_on_(g_scope_on) {
+  g_scope_base = base;
+  g_scope_cap = cap;
+  g_scope_on = true;
+}
+
+ScratchScope::~ScratchScope() {
+  g_scope_base = prev_base_;
+  g_scope_cap = prev_cap_;
+  g_scope_on = prev_on_;
+}
+
+void tag_weight(const void *p, size_t bytes, int kind, int out, int in) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  const uintptr_t a = (uintptr_t)p;
+  untag_locked(a, a + bytes);
+  g_tags[a] = Tag{a + bytes, kind, out, in};
+}
+
+void untag_range(const void *p, size_t bytes) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  untag_locked((uintptr_t)p, (uintptr_t)p + bytes);
+}
+
+int check_weight(const char *who, const void *p, int kind, int out, int in) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  auto it = g_tags.find((uintptr_t)p);
+  if (it == g_tags.end())
+    return fail(FHIP_EINVAL,
+                "%s: %p is not a tiled %s weight (upload it with fhip_*_upload or lay it out "
+                "with fhip_*_repack; raw GGUF bytes are not accepted)",
+                who, p, kind_name(kind));
+  const Tag &t = it->second;
+  if (t.kind != kind || t.out != out || t.in != in)
+    return fail(FHIP_EINVAL, "%s: %p holds a tiled %s weight [%d, %d], not %s [%d, %d]", who, p,
+                kind_name(t.kind), t.out, t.in, kind_name(kind), out, in);
+  return FHIP_OK;
+}
+
+int check_disjoint(const char *who, const void *a, size_t na, const void *b, size_t nb) {
+  const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+  if (na && nb && a0 < b0 + nb && b0 < a0 + na)
+    return fail(FHIP_EINVAL, "%s: an input buffer overlaps the scratch region of the call", who);
+  return FHIP_OK;
 }
 
 }  // namespace fhip
@@ -97,6 +188,19 @@ int fhip_init(char *name, int namelen, int *arch, size_t *total_mem) {
                 prop.gcnArchName);
   g_cus = prop.multiProcessorCount;
   g_lds = (int)prop.sharedMemPerBlock;
+  // Tuning overrides are read here once, never per call. FAK_HIP_GEMV16_FROM only names a width
+  // the two small-M kernels can both take (2..5); anything else keeps the rule.
+  g_tuning.gemv_tw = env_knob("FAK_HIP_GEMV_TW");
+  g_tuning.gemv_kw = env_knob("FAK_HIP_GEMV_KW");
+  g_tuning.gemv_globalx = env_knob("FAK_HIP_GEMV_GLOBALX");
+  const int from16 = env_knob("FAK_HIP_GEMV16_FROM");
+  g_tuning.gemv16_from = from16 >= 2 && from16 <= 5 ? from16 : 0;
+  g_tuning.gemm32_form = env_knob("FAK_HIP_GEMM32_FORM");
+  g_tuning.gemm32_sk = env_knob("FAK_HIP_GEMM32_SK");
+  g_tuning.gemm32_nwb = env_knob("FAK_HIP_GEMM32_NWB");
+  g_tuning.i8r_kw = env_knob("FAK_HIP_I8R_KW");
+  g_tuning.q8_tw = env_knob("FAK_HIP_Q8_TW");
+  g_tuning.q8_kw = env_knob("FAK_HIP_Q8_KW");
   if (name && namelen > 0) {
     strncpy(name, prop.name, (size_t)namelen - 1);
     name[namelen - 1] = 0;
@@ -151,6 +255,7 @@ void fhip_free(void *d) {
   std::lock_guard<std::mutex> lk(g_pool_mu);
   auto it = g_live.find(d);
   if (it == g_live.end()) return;  // not ours: ignore rather than corrupt the pool
+  untag_locked((uintptr_t)d, (uintptr_t)d + it->second);
   g_free.emplace(it->second, d);
   g_free_bytes += it->second;
   g_live.erase(it);
@@ -173,6 +278,7 @@ int fhip_h2d(void *d, const void *h, size_t bytes) {
   clear_error();
   if (bytes == 0) return FHIP_OK;
   if (!d || !h) return fail(FHIP_EINVAL, "fhip_h2d: null pointer");
+  untag_range(d, bytes);
   FHIP_CHECK(hipMemcpy(d, h, bytes, hipMemcpyHostToDevice));
   return FHIP_OK;
 }
@@ -190,8 +296,16 @@ int fhip_d2d(void *dst, const void *src, size_t bytes) {
   clear_error();
   if (bytes == 0) return FHIP_OK;
   if (!dst || !src) return fail(FHIP_EINVAL, "fhip_d2d: null pointer");
+  Tag copy{0, 0, 0, 0};
+  {
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    auto it = g_tags.find((uintptr_t)src);
+    if (it != g_tags.end() && it->second.end - it->first == bytes) copy = it->second;
+    untag_locked((uintptr_t)dst, (uintptr_t)dst + bytes);
+  }
   FHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_stream));
   FHIP_CHECK(hipStreamSynchronize(g_stream));
+  if (copy.kind) tag_weight(dst, bytes, copy.kind, copy.out, copy.in);
   return FHIP_OK;
 }
 
@@ -205,6 +319,7 @@ int fhip_h2d_async(void *d, const void *h, size_t bytes) {
   clear_error();
   if (bytes == 0) return FHIP_OK;
   if (!d || !h) return fail(FHIP_EINVAL, "fhip_h2d_async: null pointer");
+  untag_range(d, bytes);
   FHIP_CHECK(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, g_stream));
   return FHIP_OK;
 }
@@ -221,6 +336,7 @@ int fhip_memset_async(void *d, int value, size_t bytes) {
   clear_error();
   if (bytes == 0) return FHIP_OK;
   if (!d) return fail(FHIP_EINVAL, "fhip_memset_async: null pointer");
+  untag_range(d, bytes);
   FHIP_CHECK(hipMemsetAsync(d, value, bytes, g_stream));
   return FHIP_OK;
 }
@@ -238,6 +354,12 @@ int fhip_stream_destroy(void *s) {
   clear_error();
   if (!s) return FHIP_OK;
   if ((hipStream_t)s == g_stream) g_stream = nullptr;
+  // Its workspace is retired, not freed: a graph captured on the stream may still use it.
+  auto it = g_ws.find((hipStream_t)s);
+  if (it != g_ws.end()) {
+    if (it->second.buf) g_ws_retired.push_back(it->second.buf);
+    g_ws.erase(it);
+  }
   FHIP_CHECK(hipStreamDestroy((hipStream_t)s));
   return FHIP_OK;
 }

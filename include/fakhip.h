@@ -17,10 +17,21 @@
  *   - All launches and async copies go to the library's current stream (fhip_set_stream; the
  *     null/default stream until set). Calls are NOT thread-safe: the host serializes them,
  *     exactly as the CUDA tenant's single cudaMu mutex does (internal/compute/cuda.go:40-43).
- *   - Weights are uploaded once in a backend-private "tiled" layout (fhip_q4k_repack /
- *     fhip_q8_0_repack). The layout is a lossless byte permutation of the GGUF blocks (the
- *     exact inverse is fhip_*_unpack); it costs the same 144 B per 256 Q4_K weights and 34 B per
- *     32 Q8_0 weights, padded only to a multiple of 16 output rows.
+ *     Work queued on different streams may run concurrently: the library keeps one scratch
+ *     workspace per stream, so matmuls on two streams never share scratch.
+ *   - Weights are uploaded once in a backend-private "tiled" layout (fhip_*_upload /
+ *     fhip_*_repack). The layout is a lossless byte permutation of the GGUF blocks (the exact
+ *     inverse is fhip_*_unpack); it costs the same 144 B per 256 Q4_K weights, 210 B per 256
+ *     Q6_K weights and 34 B per 32 Q8_0 weights, padded only to a multiple of 16 output rows.
+ *     The library records the format and shape of every tiled weight it lays out; the matmul,
+ *     unpack and dequant entries return FHIP_EINVAL for a pointer that does not start a tiled
+ *     weight of the format and [out, in] they are given (raw GGUF bytes, another shape, a freed
+ *     or overwritten buffer). Writing into a tiled weight through fhip_h2d / fhip_h2d_async /
+ *     fhip_memset_async / a partial fhip_d2d, or freeing it, drops the record; an fhip_d2d of a
+ *     whole tiled weight records the copy as the same weight.
+ *   - Launch-shape overrides (FAK_HIP_GEMV_TW/_KW, FAK_HIP_GEMV_GLOBALX, FAK_HIP_GEMV16_FROM,
+ *     FAK_HIP_GEMM32_FORM/_SK/_NWB, FAK_HIP_I8R_KW, FAK_HIP_Q8_TW/_KW) are read from the
+ *     environment by fhip_init only, never per call.
  */
 #ifndef FAK_HIP_BACKEND_H
 #define FAK_HIP_BACKEND_H
@@ -39,8 +50,9 @@ extern "C" {
 /* ---- runtime ----------------------------------------------------------------------------- */
 
 /* Select device 0, verify it is gfx950, and report its name (up to namelen-1 chars), gfx
- * arch number (e.g. 950) and total memory. Idempotent. Replaces fcuda_init
- * (internal/compute/cuda_backend.h:25). Non-zero when no gfx950 device is reachable. */
+ * arch number (e.g. 950) and total memory; (re)read the launch-shape overrides. Idempotent.
+ * Replaces fcuda_init (internal/compute/cuda_backend.h:25). Non-zero when no gfx950 device is
+ * reachable. */
 int fhip_init(char *name, int namelen, int *arch, size_t *total_mem);
 /* Replaces fcuda_mem_info (cuda_backend.h:28). */
 int fhip_mem_info(size_t *free_mem, size_t *total_mem);
@@ -68,7 +80,9 @@ int fhip_memset_async(void *d, int value, size_t bytes);
 
 /* Streams and events (the CUDA tenant has one global g_stream, cuda_kernels.cu:28-32; this
  * backend exposes the stream as a handle so a host can overlap work or capture graphs).
- * Streams are created at the default priority. */
+ * Streams are created at the default priority. Each stream gets its own scratch workspace on
+ * first use; destroying a stream retires (does not free) it, since a graph captured on the
+ * stream may still use it. */
 int fhip_stream_create(void **stream);
 int fhip_stream_destroy(void *stream);
 /* Make `stream` (NULL = the default stream) the target of every later launch and async copy. */
@@ -110,7 +124,8 @@ int fhip_q4k_dequant_f32(float *dW, const void *dPacked, int out, int in);
 void *fhip_q4k_upload(const uint8_t *hRaw, int out, int in);
 /* Y[P,out] = X[P,in] @ W[out,in]^T with W a tiled Q4_K weight, X and Y row-major f32 — the
  * replacement for fcuda_q4k_matmul_f32 (internal/compute/cuda_backend.h:120), which took the
- * raw bytes; this one takes the tiled buffer fhip_q4k_upload / fhip_q4k_repack produced.
+ * raw bytes; this one takes the tiled buffer fhip_q4k_upload / fhip_q4k_repack produced and
+ * returns FHIP_EINVAL for anything else (see Conventions).
  * P <= 16 runs the small-M GEMV (decode / speculative verify); larger P runs the MFMA GEMM.
  * Error bound vs the f32 reference: GEMV max|dY|/RMS(Y) <= 1e-3, GEMM <= 1e-2. */
 int fhip_q4k_matmul_f32(const void *dPacked, const float *dX, float *dY, int out, int in,

@@ -1,9 +1,56 @@
 """Small helpers for GPU tests: numpy <-> device buffers through the fakhip C ABI only."""
 from __future__ import annotations
 
+import contextlib
+
 import numpy as np
 
 from fak_amd import fakhip
+
+
+@contextlib.contextmanager
+def knobs(monkeypatch, **env):
+    """Set FAK_HIP_* launch-shape overrides for the block. The library reads them once in
+    fhip_init, so the block re-initialises on entry and again on exit."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, str(v))
+    fakhip.init()
+    try:
+        yield
+    finally:
+        for k in env:
+            monkeypatch.delenv(k, raising=False)
+        fakhip.init()
+
+
+def rel_err_rows(got: np.ndarray, ref: np.ndarray) -> float:
+    """The reference metric per token row (max over rows), so a row of tiny activations is judged
+    against its own scale rather than hidden under a row of huge ones."""
+    got = np.atleast_2d(got)
+    ref = np.atleast_2d(ref)
+    return max(rel_err(g, r) for g, r in zip(got, ref))
+
+
+def scaled_activations(P: int, K: int, seed: int, pattern: str) -> np.ndarray:
+    """N(0,1) activations reshaped to stress the activation scaling of every route:
+    'big' rows x 1e5 (beyond f16), 'tiny' rows x 1e-20 (below f16), 'mixed' rows whose 32-value
+    blocks alternate x 1e4 / x 1e-20, 'outlier' rows with one value of 7e4 (>= 65504), and 'all'
+    cycling through the four by row."""
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((P, K)).astype(np.float32)
+    kinds = ["big", "tiny", "mixed", "outlier"] if pattern == "all" else [pattern]
+    for t in range(P):
+        k = kinds[t % len(kinds)]
+        if k == "big":
+            X[t] *= np.float32(1e5)
+        elif k == "tiny":
+            X[t] *= np.float32(1e-20)
+        elif k == "mixed":
+            f = np.where((np.arange(K) // 32) % 2 == 0, 1e4, 1e-20).astype(np.float32)
+            X[t] *= f
+        elif k == "outlier":
+            X[t, (7 * t + 5) % K] = np.float32(7e4)
+    return X
 
 
 class Dev:

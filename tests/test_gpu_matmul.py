@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from fak_amd import synth
-from tests.gpu_util import q4k_matmul, q8_0_matmul, rel_err, cosine
+from tests.gpu_util import cosine, knobs, q4k_matmul, q8_0_matmul, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -55,31 +55,73 @@ def test_q4k_gemv_7b_ffn(hip, oracle_mod, out, in_):
     _check_q4k(oracle_mod, out, in_, 1, seed=2024 + out, tol=GEMV_TOL)
 
 
-@pytest.mark.parametrize("sk", [2, 3, 4, 8])
-@pytest.mark.parametrize("out,in_,P", [(33, 4096, 1), (100, 9472, 2), (3584, 18944, 1),
-                                       (40, 2048, 4), (7, 8192, 3)])
-def test_q4k_gemv_split_k(hip, oracle_mod, monkeypatch, sk, out, in_, P):
-    """K split across workgroups (FAK_HIP_GEMV_SK forces the split): ragged splits (37 super-
-    blocks over 3, 4, 8), one super-block per split, partial tiles, 1..4 tokens."""
-    monkeypatch.setenv("FAK_HIP_GEMV_SK", str(sk))
-    _check_q4k(oracle_mod, out, in_, P, seed=out + in_ + P + sk, tol=GEMV_TOL)
+def test_q4k_lm_head_7b(hip, oracle_mod):
+    """The largest matmul of a Qwen2.5-7B decode token, a Q4_K lm_head 3584 -> 152064 (306 MB),
+    every output checked."""
+    _check_q4k(oracle_mod, 152064, 3584, 1, seed=152064, tol=GEMV_TOL)
 
 
-def test_q4k_gemv_split_k_repeatable(hip, monkeypatch):
-    """The split-K reduction sums parts in a fixed order and resets its tile counters: repeated
-    calls (and calls with another split) give bit-identical results for the same split."""
-    out, in_ = 224 * 16, 74 * 256
-    raw = synth.q4k_weights(out, in_, seed=5)
-    X = synth.activations(1, in_, seed=6)
-    monkeypatch.setenv("FAK_HIP_GEMV_SK", "4")
-    a = q4k_matmul(raw, out, in_, X, 1)
-    b = q4k_matmul(raw, out, in_, X, 1)
-    monkeypatch.setenv("FAK_HIP_GEMV_SK", "2")
-    q4k_matmul(raw, out, in_, X, 1)
-    monkeypatch.setenv("FAK_HIP_GEMV_SK", "4")
-    c = q4k_matmul(raw, out, in_, X, 1)
-    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
-    assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+@pytest.mark.parametrize("out,in_,P", [(5120, 25600, 2), (3584, 18944, 3), (3584, 18944, 4)])
+def test_q4k_gemv_global_operands_natural(hip, oracle_mod, out, in_, P):
+    """Shapes whose activation operands do not fit in LDS, so the GEMV takes its global-operand
+    path by itself: the 27B down projection at 2 tokens, the 7B one at 3 and 4."""
+    _check_q4k(oracle_mod, out, in_, P, seed=out + in_ + 7 * P, tol=GEMV_TOL)
+
+
+@pytest.mark.parametrize("P", [1, 2, 4])
+@pytest.mark.parametrize("out,in_", [(18944, 3584), (3584, 18944)])
+def test_q4k_gemv_global_operands_forced(hip, oracle_mod, monkeypatch, out, in_, P):
+    """FAK_HIP_GEMV_GLOBALX=1 forces the global-operand path on the C2 shapes; it is also
+    bit-identical to the LDS path (same operands, same order)."""
+    raw = synth.q4k_weights(out, in_, seed=out + P)
+    X = synth.activations(P, in_, seed=in_ + P)
+    lds = q4k_matmul(raw, out, in_, X, P)
+    with knobs(monkeypatch, FAK_HIP_GEMV_GLOBALX=1):
+        glob = q4k_matmul(raw, out, in_, X, P)
+    ref = oracle_mod.q4k_gemm(raw, out, in_, X, P, workers=16)
+    assert rel_err(glob, ref) <= GEMV_TOL
+    assert np.array_equal(lds.view(np.uint32), glob.view(np.uint32))
+
+
+def test_q4k_gemv16_from_knob_is_clamped(hip, oracle_mod, monkeypatch):
+    """FAK_HIP_GEMV16_FROM names the first width on the 5..16-token kernel; values the int8
+    kernel cannot take (it holds 1..4 tokens) are ignored, so 6 tokens still get every row."""
+    out, in_, P = 512, 2048, 6
+    raw = synth.q4k_weights(out, in_, seed=66)
+    X = synth.activations(P, in_, seed=67)
+    with knobs(monkeypatch, FAK_HIP_GEMV16_FROM=8):
+        Y = q4k_matmul(raw, out, in_, X, P)
+    assert rel_err(Y, oracle_mod.q4k_gemm(raw, out, in_, X, P)) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("pattern", ["big", "tiny", "mixed", "outlier"])
+@pytest.mark.parametrize("out,in_,P", [(1024, 3584, 1), (512, 2048, 4), (512, 2048, 64)])
+def test_q4k_activation_scales(hip, oracle_mod, out, in_, P, pattern):
+    """Activations far outside f16 (x 1e5, a lone 7e4), far below it (x 1e-20) and mixed within
+    a row: every token row within its route's bound of the oracle, judged per row."""
+    from tests.gpu_util import rel_err_rows, scaled_activations
+    print(f"[case] q4k scales out={out} in={in_} P={P} {pattern}", flush=True)
+    raw = synth.q4k_weights(out, in_, seed=out + P)
+    X = scaled_activations(P, in_, 3 * P + 1, pattern)
+    Y = q4k_matmul(raw, out, in_, X, P)
+    ref = oracle_mod.q4k_gemm(raw, out, in_, X, P, workers=16)
+    e = rel_err_rows(Y, ref)
+    print(f"    per-row max|d|/RMS = {e:.3e}", flush=True)
+    assert e <= (GEMV_TOL if P <= 16 else GEMM_TOL), e
+
+
+@pytest.mark.parametrize("pattern", ["big", "tiny", "mixed", "outlier", "all"])
+@pytest.mark.parametrize("P", [1, 4, 8, 16, 40])
+def test_q8_0_activation_scales(hip, oracle_mod, P, pattern):
+    from tests.gpu_util import rel_err_rows, scaled_activations
+    out, in_ = 1536, 576
+    print(f"[case] q8_0 scales P={P} {pattern}", flush=True)
+    raw = synth.q8_0_weights(out, in_, seed=P + 9)
+    X = scaled_activations(P, in_, P, pattern)
+    Y = q8_0_matmul(raw, out, in_, X, P)
+    e = rel_err_rows(Y, oracle_mod.q8_0_gemm(raw, out, in_, X, P))
+    print(f"    per-row max|d|/RMS = {e:.3e}", flush=True)
+    assert e <= GEMV_TOL, e
 
 
 @pytest.mark.parametrize("P", [1, 3, 4, 8, 16])
@@ -112,15 +154,13 @@ def test_q4k_gemm_forms_bit_identical(hip, oracle_mod, monkeypatch, out, in_, P)
     print(f"[case] gemm forms out={out} in={in_} P={P}", flush=True)
     raw = synth.q4k_weights(out, in_, seed=out + 3 * P)
     X = synth.activations(P, in_, seed=P + 5)
-    monkeypatch.setenv("FAK_HIP_GEMM32_FORM", "1")
-    Y1 = q4k_matmul(raw, out, in_, X, P)
-    monkeypatch.setenv("FAK_HIP_GEMM32_FORM", "2")
-    Y2 = q4k_matmul(raw, out, in_, X, P)
-    monkeypatch.setenv("FAK_HIP_GEMM32_FORM", "3")
-    monkeypatch.setenv("FAK_HIP_GEMM32_SK", "1")  # no K split: the same summation order
-    Y3 = q4k_matmul(raw, out, in_, X, P)
-    monkeypatch.delenv("FAK_HIP_GEMM32_SK")
-    monkeypatch.delenv("FAK_HIP_GEMM32_FORM")
+    with knobs(monkeypatch, FAK_HIP_GEMM32_FORM=1):
+        Y1 = q4k_matmul(raw, out, in_, X, P)
+    with knobs(monkeypatch, FAK_HIP_GEMM32_FORM=2):
+        Y2 = q4k_matmul(raw, out, in_, X, P)
+    # the default form with no K split: the same summation order
+    with knobs(monkeypatch, FAK_HIP_GEMM32_FORM=3, FAK_HIP_GEMM32_SK=1):
+        Y3 = q4k_matmul(raw, out, in_, X, P)
     assert np.array_equal(Y1.view(np.uint32), Y2.view(np.uint32))
     assert np.array_equal(Y1.view(np.uint32), Y3.view(np.uint32))
     if out > 4096:

@@ -41,9 +41,13 @@ def dev_mlp(gate, up, down, H, I, X, P, q6):
 
 
 @pytest.mark.parametrize("q6", [False, True], ids=["q4down", "q6down"])
-@pytest.mark.parametrize("H,I,P", [(3584, 18944, 1), (512, 1024, 1), (512, 1024, 2),
+@pytest.mark.parametrize("H,I,P", [(3584, 18944, 1), (3584, 18944, 2), (3584, 18944, 3),
+                                   (3584, 18944, 4), (512, 1024, 1), (512, 1024, 2),
                                    (256, 768, 3), (1024, 2816, 4), (768, 256, 1)])
 def test_mlp_matches_oracle(hip, oracle_mod, H, I, P, q6):
+    """At the 7B shape with 2..4 tokens the down projection's own scratch (K-range partials of
+    the Q6_K kernel, global activation operands of the Q4_K one) is large: it must not land on
+    the intermediate the down GEMV is reading."""
     print(f"[mlp] H={H} I={I} P={P} q6={q6}", flush=True)
     gate, up, down = weights(H, I, 10 * H + I + P, q6)
     X = synth.activations(P, H, 5 + P)
