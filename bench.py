@@ -1,20 +1,24 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 Q4_K / Q8_0 matmul backend (one GPU), in the style of fak's
 cmd/q8kernel / cmd/q8bench: seeded synthetic weights of each workload's shape, warm-up, timed
-launches with HIP events, a JSON report.
+launches with HIP events, correctness against the oracle in the same run, a JSON report.
 
 The headline line (`value`) is the Q4_K decode GEMV at the Qwen2.5-7B FFN shape: one step = the
 gate/up GEMV (K=3584 -> N=18944) plus the down GEMV (K=18944 -> N=3584) at M=1, inputs resident
 in HBM. Throughput counts algorithmic bytes: GGUF-native weight bytes (144 B per 256 weights)
 plus f32 activations and outputs, once. Every launch reads a different copy of the weights,
-rotating over more than 256 MB so the 256 MB Infinity Cache cannot serve them.
+rotating over more than 256 MB so the 256 MB Infinity Cache cannot serve them. `roofline` is
+the dominant (slower) kernel of the step, launched back to back.
 
-The other workloads are reported under "workloads": Q8_0 GEMV 576->1536, the prefill GEMM at
+The other workloads are reported under "workloads", each with its error against the oracle
+(max|dY|/RMS, cosine, largest per-element relative error): Q8_0 GEMV 576->1536 (single launch,
+back to back, and one graph of 300 launches over 300 weight copies), the prefill GEMM at
 M=128/512/2048 (TFLOP/s vs the 2.5 PFLOP/s dense f16 MFMA peak), the 28-layer Qwen2.5-7B decode
 matmul set (tokens/s bound by matmul time) and the 27B-class small-M verify widths.
 
-`cpu_baseline` times the oracle (the C restatement of the reference's Go CPU GEMV, row-parallel
-over the host cores) on the same C2 inputs.
+`cpu_baseline` times the oracle (the C restatement of the reference's Go CPU path, row-parallel
+like parForRange, built -O3 -ffp-contract=off -fno-fast-math) on the same inputs on this host's
+cores, for every workload.
 
     python bench.py [--steps K] [--warmup W] [--quick] [--no-cpu]
 """
@@ -37,6 +41,8 @@ from fak_amd import fakhip, synth  # noqa: E402
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16 MFMA
 ROTATE_BYTES = 300 << 20    # > 256 MB Infinity Cache
+MIN_COPIES = 9              # at least this many distinct weight copies per rotating workload
+CPU_THREADS_MAX = 16        # the host-CPU share of one GPU on the benchmark boxes
 METRIC = "Q4_K decode GEMV HBM GB/s (% peak); prefill GEMM TFLOP/s (% MFMA peak)"
 
 
@@ -116,7 +122,28 @@ class Buf:
 
 
 def copies_for(nbytes):
-    return max(2, -(-ROTATE_BYTES // max(nbytes, 1)))
+    return max(MIN_COPIES, -(-ROTATE_BYTES // max(nbytes, 1)))
+
+
+def check(got, ref):
+    """Error of a device result against the oracle: the reference's max|d|/RMS(ref) metric
+    (internal/model/quant_q4k_test.go:140-158), the cosine, and the largest per-element relative
+    error over elements with |ref| > 1e-3 RMS(ref)."""
+    got = np.asarray(got, np.float64).ravel()
+    ref = np.asarray(ref, np.float64).ravel()
+    rms = float(np.sqrt(np.mean(ref * ref)))
+    d = np.abs(got - ref)
+    big = np.abs(ref) > 1e-3 * rms
+    cos = float(got @ ref / (np.linalg.norm(got) * np.linalg.norm(ref)))
+    return {"max_abs_over_rms": float(d.max() / rms), "cosine": round(cos, 9),
+            "max_rel_elem": float((d[big] / np.abs(ref[big])).max()) if big.any() else 0.0}
+
+
+def sample_rows(raw, n, k, rows):
+    """The first and last rows/2 rows of a raw Q4_K weight: (sub-weight bytes, row indices)."""
+    rb = (k // 256) * 144
+    sel = np.concatenate([np.arange(0, rows // 2), np.arange(n - rows // 2, n)])
+    return np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel]), sel
 
 
 def time_calls(calls, steps, warmup, ev):
@@ -166,15 +193,16 @@ def time_one(call, steps, warmup, ev):
 
 
 def traffic_from_profiles():
-    """HBM bytes per gate/up launch from the committed FETCH_SIZE / WRITE_SIZE counter runs
-    (profiles/q4k_gemv_traffic.json), or None when absent."""
+    """HBM bytes per launch of each decode GEMV from the committed FETCH_SIZE / WRITE_SIZE counter
+    runs (profiles/q4k_gemv_traffic.json: {"per_kernel": {"gate_up": B, "down": B}, ...}), or
+    an empty mapping when absent."""
     path = os.path.join(ROOT, "profiles", "q4k_gemv_traffic.json")
     try:
         with open(path) as f:
             t = json.load(f)
-        return t["hbm_bytes_per_launch"], t
-    except (OSError, KeyError, ValueError):
-        return None, None
+        return t.get("per_kernel", {}), t
+    except (OSError, ValueError):
+        return {}, None
 
 
 def bench_gemv_pair(steps, warmup, ev, seed=7):
@@ -196,6 +224,13 @@ def bench_gemv_pair(steps, warmup, ev, seed=7):
     ms, per = time_calls(calls, steps, warmup, ev)
     alg = [q4k_bytes(n, k) + 4 * (n + k) for n, k in shapes]
     single = [time_one(c, steps, warmup, ev) for c in calls]
+    # correctness: every output of both shapes against the oracle on the same inputs
+    import oracle  # the checker
+    checks = []
+    for w, (x, xb), yb in zip(ws, xs, ys):
+        fakhip.call("fhip_q4k_matmul_f32", w.ptrs[0], xb.ptr, yb.ptr, w.n, w.k, 1)
+        checks.append(check(yb.host(), oracle.q4k_matrows(w.raw, w.n, w.k, x[0],
+                                                           workers=cpu_threads())))
     res = {
         "ms_per_step": ms,
         "per_call_us": [1e3 * p for p in per],
@@ -203,47 +238,84 @@ def bench_gemv_pair(steps, warmup, ev, seed=7):
         "b2b_GBs": [a / (p * 1e6) for a, p in zip(alg, single)],
         "alg_bytes": alg,
         "copies": [len(w.ptrs) for w in ws],
+        "check": {"gate_up": checks[0], "down": checks[1]},
     }
-    return res, ws, xs, ys
+    cpu_in = [(w.raw, w.n, w.k, x[0]) for w, (x, _) in zip(ws, xs)]
+    for w in ws:
+        w.free()
+    for _, b in xs:
+        b.free()
+    for b in ys:
+        b.free()
+    return res, cpu_in
 
 
-def bench_q8_0(steps, warmup, ev):
+def bench_q8_0(steps, warmup, ev, graph_copies=300):
+    """C1: Q8_0 GEMV 576 -> 1536 (0.95 MB, launch-bound): one launch alone, launches back to back,
+    and one graph of `graph_copies` launches, each over its own weight copy (> 256 MB in all, so
+    the Infinity Cache cannot serve them), replayed."""
     n, k = 1536, 576
-    w = Weight("q8", n, k, 1, copies_for(q8_bytes(n, k)))
+    w = Weight("q8", n, k, 1, max(graph_copies, copies_for(q8_bytes(n, k))))
     x = synth.activations(1, k, 2)
     xb, yb = Buf(x.nbytes, x), Buf(n * 4)
     calls = [("fhip_q8_0_matmul_f32", lambda i: (w.ptrs[i % len(w.ptrs)], xb.ptr, yb.ptr, n, k, 1))]
     ms, per = time_calls(calls, steps, warmup, ev)
     alg = q8_bytes(n, k) + 4 * (n + k)
+    gcalls = [("fhip_q8_0_matmul_f32", lambda i, j=j: (w.ptrs[j], xb.ptr, yb.ptr, n, k, 1))
+              for j in range(graph_copies)]
+    graph_ms = decode_graph_ms(gcalls, max(5, steps // 20), 2, ev)
+    import oracle  # the checker
+    fakhip.call("fhip_q8_0_matmul_f32", w.ptrs[0], xb.ptr, yb.ptr, n, k, 1)
+    chk = check(yb.host(), oracle.q8_0_matrows(w.raw, n, k, x[0]))
     w.free(), xb.free(), yb.free()
-    return {"shape": [1, k, n], "blocks": n * (k // 32), "us_per_call": 1e3 * per[0],
-            "us_back_to_back": 1e3 * ms, "GBs_back_to_back": alg / (ms * 1e6),
-            "alg_bytes": alg}
+    return {"shape": [1, k, n], "blocks": n * (k // 32), "alg_bytes": alg,
+            "us_per_call": 1e3 * per[0], "us_back_to_back": 1e3 * ms,
+            "GBs_back_to_back": alg / (ms * 1e6),
+            "graph": {"launches": graph_copies, "weight_copies": graph_copies,
+                      "us_per_launch": 1e3 * graph_ms / graph_copies,
+                      "GBs": graph_copies * alg / (graph_ms * 1e6)},
+            "check": chk}, (w.raw, n, k, x[0])
 
 
 def bench_gemm(M, steps, warmup, ev):
+    """C3: prefill GEMM K=3584 -> N=18944 at M tokens, weights rotating over >= 9 copies;
+    checked on 256 sampled output rows."""
     n, k = 18944, 3584
-    w = Weight("q4k", n, k, 3, 2)
+    w = Weight("q4k", n, k, 3, copies_for(q4k_bytes(n, k)))
     X = synth.activations(M, k, 4)
     xb, yb = Buf(X.nbytes, X), Buf(M * n * 4)
     calls = [("fhip_q4k_matmul_f32", lambda i: (w.ptrs[i % len(w.ptrs)], xb.ptr, yb.ptr, n, k, M))]
     ms, per = time_calls(calls, steps, warmup, ev)
     flops = 2.0 * M * n * k
     t = per[0] * 1e-3
+    import oracle  # the checker
+    fakhip.call("fhip_q4k_matmul_f32", w.ptrs[0], xb.ptr, yb.ptr, n, k, M)
+    sub, sel = sample_rows(w.raw, n, k, 256)
+    chk = check(yb.host().reshape(M, n)[:, sel], oracle.q4k_gemm(sub, len(sel), k, X, M,
+                                                                  workers=cpu_threads()))
+    res = {"M": M, "us_per_call": 1e3 * per[0], "us_back_to_back": 1e3 * ms,
+           "TFLOPs": flops / t / 1e12, "pct_mfma_peak": 100.0 * flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS,
+           "weight_copies": len(w.ptrs), "check": dict(chk, rows_checked=len(sel))}
+    cpu_in = (w.raw, n, k, X, M)
     w.free(), xb.free(), yb.free()
-    return {"M": M, "us_per_call": 1e3 * per[0], "TFLOPs": flops / t / 1e12,
-            "pct_mfma_peak": 100.0 * flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS}
+    return res, cpu_in
 
 
 def bench_small_m(steps, warmup, ev):
+    """C5: the 27B-class FFN pair (gate/up 5120 -> 25600, down 25600 -> 5120) at the verify widths
+    M = 1, 4, 8, 16; every output of both shapes checked."""
+    import oracle  # the checker
     out = []
+    cpu_in = []
     shapes = [(25600, 5120), (5120, 25600)]
     ws = [Weight("q4k", n, k, 20 + i, copies_for(q4k_bytes(n, k))) for i, (n, k) in enumerate(shapes)]
     for M in (1, 4, 8, 16):
         bufs = []
         calls = []
+        Xs = []
         for (n, k), w in zip(shapes, ws):
             X = synth.activations(M, k, 30 + M)
+            Xs.append(X)
             xb, yb = Buf(X.nbytes, X), Buf(M * n * 4)
             bufs += [xb, yb]
             calls.append(("fhip_q4k_matmul_f32",
@@ -252,13 +324,20 @@ def bench_small_m(steps, warmup, ev):
         ms, per = time_calls(calls, steps, warmup, ev)
         alg = sum(q4k_bytes(n, k) + 4 * M * (n + k) for n, k in shapes)
         gbs = alg / (sum(per) * 1e6)
-        out.append({"M": M, "us_pair": 1e3 * sum(per), "GBs": gbs,
-                    "pct_hbm_peak": 100.0 * gbs / HBM_PEAK_GBS})
+        chk = {}
+        for (n, k), w, X, name, yb in zip(shapes, ws, Xs, ("gate_up", "down"), bufs[1::2]):
+            fakhip.call("fhip_q4k_matmul_f32", w.ptrs[0], bufs[0 if name == "gate_up" else 2].ptr,
+                        yb.ptr, n, k, M)
+            chk[name] = check(yb.host(), oracle.q4k_gemm(w.raw, n, k, X, M, workers=cpu_threads()))
+        out.append({"M": M, "us_pair": 1e3 * sum(per), "per_call_us": [1e3 * p for p in per],
+                    "GBs": gbs, "pct_hbm_peak": 100.0 * gbs / HBM_PEAK_GBS, "check": chk})
+        cpu_in.append((M, Xs))
         for b in bufs:
             b.free()
+    raws = [(w.raw, w.n, w.k) for w in ws]
     for w in ws:
         w.free()
-    return out
+    return out, (raws, cpu_in)
 
 
 def bench_int8_route(steps, warmup, ev):
@@ -423,7 +502,8 @@ def bench_decode_stack(steps, warmup, ev, layers=28):
             ptrs.append(p)
         per_layer.append(ptrs)
     head = Weight("q4k", V, H, 60, 1)
-    xs = {k: Buf(k * 4, synth.activations(1, k, 70 + k)[0]) for k in (H, F)}
+    xs_host = {k: synth.activations(1, k, 70 + k)[0] for k in (H, F)}
+    xs = {k: Buf(k * 4, xs_host[k]) for k in (H, F)}
     ys = {n: Buf(n * 4) for n in (H, KV, F, V)}
     ys_v = Buf(KV * 4)  # v's output (k uses ys[KV]) so a group's members never share an output
     calls = []
@@ -460,6 +540,17 @@ def bench_decode_stack(steps, warmup, ev, layers=28):
     graph_ms = decode_graph_ms(gcalls, steps, warmup, ev)
     wbytes = layers * sum(q4k_bytes(n, k) for n, k in layer_shapes) + q4k_bytes(V, H)
     abytes = layers * sum(4 * (n + k) for n, k in layer_shapes) + 4 * (V + H)
+    # correctness: the lm_head and the last layer's down projection, every output
+    import oracle  # the checker
+    chk = {}
+    fakhip.call("fhip_q4k_matmul_f32", head.ptrs[0], xs[H].ptr, ys[V].ptr, V, H, 1)
+    chk["lm_head"] = check(ys[V].host(), oracle.q4k_matrows(head.raw, V, H, xs_host[H],
+                                                            workers=cpu_threads()))
+    fakhip.call("fhip_q4k_matmul_f32", per_layer[-1][6], xs[F].ptr, ys[H].ptr, H, F, 1)
+    chk["down"] = check(ys[H].host(), oracle.q4k_matrows(base[6].raw, H, F, xs_host[F],
+                                                         workers=cpu_threads()))
+    cpu_in = ([(w.raw, n, k) for w, (n, k) in zip(base, layer_shapes)], (head.raw, V, H), xs_host,
+              layers)
     for l in range(1, layers):
         for p in per_layer[l]:
             fakhip.load().fhip_free(p)
@@ -467,7 +558,7 @@ def bench_decode_stack(steps, warmup, ev, layers=28):
         w.free()
     for b in list(xs.values()) + list(ys.values()) + [ys_v]:
         b.free()
-    return {"layers": layers, "gemvs_per_token": len(calls), "weight_bytes": wbytes,
+    return {"check": chk, "layers": layers, "gemvs_per_token": len(calls), "weight_bytes": wbytes,
             "ms_per_token": ms, "tok_per_s": 1e3 / ms,
             "GBs": (wbytes + abytes) / (ms * 1e6),
             "pct_hbm_peak": 100.0 * (wbytes + abytes) / (ms * 1e6) / HBM_PEAK_GBS,
@@ -479,34 +570,103 @@ def bench_decode_stack(steps, warmup, ev, layers=28):
             "grouped_graph": {"graph_launches_per_token": 1, "ms_per_token": graph_ms,
                               "tok_per_s": 1e3 / graph_ms,
                               "pct_hbm_peak": 100.0 * (wbytes + abytes) / (graph_ms * 1e6)
-                              / HBM_PEAK_GBS}}
+                              / HBM_PEAK_GBS}}, cpu_in
 
 
-def cpu_baseline(ws, xs, ys, budget_s=10.0):
-    """The oracle (C restatement of q4kMatRowsRange, row-parallel like parForRange) timed on the
-    same C2 inputs on this host's cores; also reports the GPU result's error against it."""
-    import oracle  # the checker: used only in this leg
-    workers = min(os.cpu_count() or 1, 16)
-    reps, t0 = 0, time.perf_counter()
+
+
+def cpu_threads():
+    """Threads of the CPU legs: the cores this process may run on, at most the 16-core host share
+    that one GPU has on the benchmark boxes."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, CPU_THREADS_MAX))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def time_cpu(fn, min_reps=3, budget_s=2.0):
+    """Median seconds of fn() after one warm-up call: at least min_reps runs, more while the
+    budget lasts (at most 20)."""
+    fn()
     times = []
-    errs = []
-    while time.perf_counter() - t0 < budget_s or reps < 2:
+    t0 = time.perf_counter()
+    while len(times) < min_reps or (time.perf_counter() - t0 < budget_s and len(times) < 20):
         ts = time.perf_counter()
-        outs = [oracle.q4k_matrows(w.raw, w.n, w.k, x, workers=workers) for w, (x, _) in zip(ws, xs)]
+        fn()
         times.append(time.perf_counter() - ts)
-        reps += 1
-        if reps == 1:
-            for w, y, ref in zip(ws, ys, outs):
-                got = y.host()
-                errs.append(float(np.max(np.abs(got - ref)) / np.sqrt(np.mean(ref.astype(np.float64) ** 2))))
-        if reps >= 50:
-            break
-    med = float(np.median(times))
-    alg = sum(q4k_bytes(w.n, w.k) + 4 * (w.n + w.k) for w in ws)
-    return {"value": alg / med / 1e9, "unit": "GB/s", "cores": workers, "kind": "port",
-            "sample": f"full C2 pair (gate/up 3584->18944 + down 18944->3584, M=1), {reps} reps, "
-                      f"median {med * 1e3:.1f} ms",
-            "gpu_max_rel_err_vs_oracle": errs}
+    return float(np.median(times)), len(times)
+
+
+def cpu_baselines(c2_in, c1_in=None, c3_in=None, c4_in=None, c5_in=None):
+    """The oracle (the C restatement of the reference's Go CPU path: q4kMatRowsRange /
+    q4kGemmRange / kQuantMatRowsRange, row-parallel like parForRange) on the same inputs as each
+    GPU workload, on cpu_threads() host threads."""
+    import oracle  # the checker, here the timed CPU path
+    W = cpu_threads()
+    q4k_rows = lambda raw, n, k, x: oracle.q4k_matrows(raw, n, k, x, workers=W)
+    # C2: the decode pair
+    t, reps = time_cpu(lambda: [q4k_rows(*a) for a in c2_in], min_reps=5)
+    alg2 = sum(q4k_bytes(n, k) + 4 * (n + k) for _, n, k, _ in c2_in)
+    base = {"value": alg2 / t / 1e9, "unit": "GB/s", "cores": W, "kind": "port",
+            "sample": f"full C2 pair (gate/up 3584->18944 + down 18944->3584, M=1), median of "
+                      f"{reps} after a warm-up: {t * 1e3:.2f} ms",
+            "host_cpus_visible": os.cpu_count(), "cpu_model": cpu_model(),
+            "build": "gcc -O3 -ffp-contract=off -fno-fast-math (oracle/build.py)"}
+    cfg = {"c2_q4k_gemv_pair": {"GBs": round(base["value"], 2), "ms_per_step": t * 1e3}}
+    if c1_in is not None:
+        raw, n, k, x = c1_in
+        t1, reps = time_cpu(lambda: oracle.q8_0_matrows(raw, n, k, x, workers=W), min_reps=20,
+                            budget_s=1.0)
+        cfg["c1_q8_0_gemv"] = {"us_per_call": t1 * 1e6, "GBs": (q8_bytes(n, k) + 4 * (n + k)) / t1 / 1e9,
+                               "sample": f"full, median of {reps}"}
+    if c3_in:
+        rows = []
+        for raw, n, k, X, M in c3_in:
+            sub, sel = sample_rows(raw, n, k, n // 8)  # 2,368 of 18,944 rows, scaled by 8
+            ts, reps = time_cpu(lambda: oracle.q4k_gemm(sub, len(sel), k, X, M, workers=W),
+                                budget_s=1.0)
+            tf = ts * n / len(sel)
+            rows.append({"M": M, "ms_per_call": tf * 1e3, "TFLOPs": 2.0 * M * n * k / tf / 1e12,
+                         "sample": f"{len(sel)} of {n} rows, median of {reps}, scaled to {n}"})
+        cfg["c3_prefill_gemm"] = rows
+    if c4_in is not None:
+        shapes, head, xs_host, layers = c4_in
+        per = []
+        for raw, n, k in shapes:
+            ts, _ = time_cpu(lambda: q4k_rows(raw, n, k, xs_host[k]), budget_s=0.5)
+            per.append(ts)
+        hr, hn, hk = head
+        th, _ = time_cpu(lambda: q4k_rows(hr, hn, hk, xs_host[hk]), budget_s=1.0)
+        tok = layers * sum(per) + th
+        wbytes = layers * sum(q4k_bytes(n, k) for _, n, k in shapes) + q4k_bytes(hn, hk)
+        cfg["c4_decode_stack"] = {"ms_per_token": tok * 1e3, "tok_per_s": 1.0 / tok,
+                                  "GBs": wbytes / tok / 1e9,
+                                  "sample": "each of the 8 distinct shapes timed (median of >= 3),"
+                                            f" summed as {layers} layers + lm_head"}
+    if c5_in is not None:
+        raws, per_m = c5_in
+        rows = []
+        for M, Xs in per_m:
+            ts, reps = time_cpu(lambda: [oracle.q4k_gemm(raw, n, k, X, M, workers=W)
+                                         for (raw, n, k), X in zip(raws, Xs)], budget_s=1.0)
+            alg = sum(q4k_bytes(n, k) + 4 * M * (n + k) for _, n, k in raws)
+            rows.append({"M": M, "ms_pair": ts * 1e3, "GBs": alg / ts / 1e9,
+                         "sample": f"full pair, median of {reps}"})
+        cfg["c5_small_m"] = rows
+    base["configs"] = cfg
+    return base
 
 
 def main():
@@ -526,50 +686,74 @@ def main():
     print(f"[bench] device {info['name']} gfx{info['arch']} "
           f"{info['total_mem'] / 2**30:.0f} GiB", file=sys.stderr, flush=True)
     ev = Events()
-    c2, ws, xs, ys = bench_gemv_pair(args.steps, args.warmup, ev)
-    print(f"[bench] C2 pair {c2['ms_per_step'] * 1e3:.2f} us/step, per call "
-          f"{[round(u, 2) for u in c2['per_call_us']]} us", file=sys.stderr, flush=True)
+    c2, c2_in = bench_gemv_pair(args.steps, args.warmup, ev)
+    print(f"[bench] C2 pair {c2['ms_per_step'] * 1e3:.2f} us/step, back to back "
+          f"{[round(u, 2) for u in c2['b2b_launch_us']]} us", file=sys.stderr, flush=True)
     alg_step = sum(c2["alg_bytes"])
     value = alg_step / (c2["ms_per_step"] * 1e6)
-    # Dominant kernel: the gate/up GEMV (one launch per call), launched back to back over the
-    # rotating weight copies and timed with one HIP event pair on its stream.
-    gate_gbs = c2["b2b_GBs"][0]
+    # Dominant kernel: the slower GEMV of the step (each call is one launch), launched back to
+    # back over its rotating weight copies and timed with one HIP event pair on its stream.
+    names = ["gate_up", "down"]
+    dom = int(np.argmax(c2["b2b_launch_us"]))
     traffic, tinfo = traffic_from_profiles()
+    kernels = {nm: {"us_back_to_back": round(c2["b2b_launch_us"][i], 3),
+                    "GBs": round(c2["b2b_GBs"][i], 1),
+                    "frac": round(c2["b2b_GBs"][i] / HBM_PEAK_GBS, 4),
+                    "hbm_bytes_per_launch": traffic.get(nm)} for i, nm in enumerate(names)}
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(c2["ms_per_step"], 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "arithmetic": "Q4_K 4-bit codes x activations carried as two int8 digits per value "
+                      "(a power-of-two scale per 32 values) on v_mfma_i32_16x16x64_i8 with exact "
+                      "int32 sums; sub-block scales, mins and accumulation in f32",
         "data": "synthetic (seeded GGUF Q4_K blocks, N(0,1) activations)",
         "config": {"workload": "Q4_K decode GEMV M=1, Qwen2.5-7B FFN: gate/up K=3584 N=18944 + "
                                "down K=18944 N=3584", "M": 1,
                    "weight_copies_rotated": c2["copies"]},
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 1),
-        "roofline": {"bound": "hbm", "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic,
-                     "kernel": "q4k_gemv_i8_kernel<1, lds> (gate/up K=3584 N=18944, M=1)",
-                     "alg_bytes_per_launch": c2["alg_bytes"][0],
-                     "launch_us": round(c2["b2b_launch_us"][0], 3),
+        "roofline": {"bound": "hbm", "achieved": round(c2["b2b_GBs"][dom], 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(c2["b2b_GBs"][dom] / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get(names[dom]),
+                     "kernel": f"q4k_gemv_i8_kernel<1, lds> ({names[dom]}: "
+                               + ("K=3584 N=18944" if dom == 0 else "K=18944 N=3584") + ", M=1)",
+                     "alg_bytes_per_launch": c2["alg_bytes"][dom],
+                     "launch_us": round(c2["b2b_launch_us"][dom], 3),
+                     "step_frac": round(value / HBM_PEAK_GBS, 4),
                      "traffic_source": tinfo.get("source") if tinfo else None},
-        "per_kernel_b2b_us": {"gate_up": round(c2["b2b_launch_us"][0], 3),
-                              "down": round(c2["b2b_launch_us"][1], 3)},
+        "per_kernel": kernels,
+        "check": c2["check"],
     }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(ws, xs, ys)
-    for w in ws:
-        w.free()
+    c1_in = c3_in = c4_in = c5_in = None
     if not args.quick:
         wl = {}
         steps = max(10, args.steps // 4)
-        wl["c1_q8_0_gemv"] = bench_q8_0(args.steps, args.warmup, ev)
-        wl["c3_prefill_gemm"] = [bench_gemm(M, steps, 3, ev) for M in (128, 512, 2048)]
-        wl["c4_decode_stack"] = bench_decode_stack(max(5, args.steps // 20), 2, ev)
-        wl["c5_small_m"] = bench_small_m(steps, 3, ev)
+        wl["c1_q8_0_gemv"], c1_in = bench_q8_0(args.steps, args.warmup, ev)
+        print(f"[bench] C1 {wl['c1_q8_0_gemv']['us_per_call']:.2f} us/call, graph "
+              f"{wl['c1_q8_0_gemv']['graph']['GBs']:.0f} GB/s", file=sys.stderr, flush=True)
+        c3, c3_in = [], []
+        for M in (128, 512, 2048):
+            r, ci = bench_gemm(M, steps, 3, ev)
+            c3.append(r)
+            c3_in.append(ci)
+            print(f"[bench] C3 M={M} {r['us_per_call']:.1f} us {r['TFLOPs']:.0f} TFLOP/s",
+                  file=sys.stderr, flush=True)
+        wl["c3_prefill_gemm"] = c3
+        wl["c4_decode_stack"], c4_in = bench_decode_stack(max(5, args.steps // 20), 2, ev)
+        print(f"[bench] C4 {wl['c4_decode_stack']['tok_per_s']:.0f} tok/s", file=sys.stderr,
+              flush=True)
+        wl["c5_small_m"], c5_in = bench_small_m(steps, 3, ev)
+        print(f"[bench] C5 {[round(r['us_pair'], 1) for r in wl['c5_small_m']]} us",
+              file=sys.stderr, flush=True)
         wl["int8_route"] = bench_int8_route(steps, 3, ev)
         wl["q6k_gemv"] = bench_q6k(steps, 3, ev)
         wl["fused_mlp"] = bench_mlp(steps, 3, ev)
         line["workloads"] = wl
+    if not args.no_cpu:
+        print(f"[bench] CPU baselines on {cpu_threads()} threads", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baselines(c2_in, c1_in, c3_in, c4_in, c5_in)
     print(json.dumps(line), flush=True)
 
 

@@ -602,7 +602,7 @@ int launch_i8_any(const GemvGroup &g, const float *X, int K, int M, bool swiglu 
 
 // First width on the 5..16-token kernel: 5, or 3 for K >= 24576, where the int8 kernel's
 // four-token workgroups measured 36-37 us on a 5120 x 25600 matrix against 30-32 us (at K = 18944
-// and at K = 5120 the int8 kernel stays 20-35% faster). FAK_HIP_GEMV16_FROM (2..5) overrides.
+// and at K = 5120 the int8 kernel stays 20-35% faster). FAK_HIP_GEMV16_FROM (1..5) overrides.
 int gemv16_from(int K) {
   const int f = tuning().gemv16_from;
   return f ? f : K >= 24576 ? 3 : 5;

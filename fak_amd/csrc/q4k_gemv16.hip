@@ -9,12 +9,16 @@
 //     nibble pair with one and-or and one packed fma: (1024 + n) * sc - 1024 * sc, or for the
 //     high nibbles masked in place (1024 + 16 n) * (sc / 16) - 64 * sc. The fma rounds once and
 //     the result is an integer below 2048, so it is exact;
-//   * activation operand: 32 operand rows, the f16 of x (rows 0..15 = tokens 0..15) and the f16
-//     of the remainder x - f16(x) (rows 16..31), so the products carry ~22 bits of x;
-//   * the min term is one more MFMA per super-block: activation rows S_s / 32 (hi and lo parts,
-//     the division keeps S within f16 range for any |x| < 65504), weight columns 32 * m_s.
-// The f32 result of a super-block is scaled by d and dmin of the lane's row and accumulated;
-// the hi and lo rows of a token are added at the end.
+//   * activation operand: 32 operand rows, the f16 of v = x / s_t (rows 0..15 = tokens 0..15) and
+//     the f16 of the remainder v - f16(v) (rows 16..31), so the products carry ~22 bits of x.
+//     s_t is a power of two per (token, K range of the workgroup) that puts the range's largest
+//     magnitude in [2^13, 2^14): any finite f32 activation becomes f16 operands without overflow
+//     and with full precision down to 2^-28 of the range's maximum;
+//   * the min term is one more MFMA per super-block: activation rows S_s / 32 (hi and lo parts;
+//     S_s / 32 <= 2^14), weight columns 32 * m_s.
+// The f32 result of a super-block is scaled by d and dmin of the lane's row and accumulated; the
+// hi and lo rows of a token are added at the end and multiplied by s_t (exact). A range holding a
+// NaN or an infinity gets s_t = NaN, which reaches every output of that token.
 //
 // Work split: a workgroup = 4 waves x 64 rows (16 tiled records of 16 rows) over one K range of
 // the weight; K is split into SK ranges of about 4 super-blocks across workgroups, and a second
@@ -43,10 +47,11 @@ __device__ __forceinline__ uint32_t as_u(h2 v) { return __builtin_bit_cast(uint3
 
 // LDS stage of one super-block b: 17 units of 64 lanes x 16 B.
 //   unit s < 16, lane l: 8 f16 of operand row v = l & 31 at K = 256 b + 16 s + 8 (l >> 5) +
-//     perm8(j): the f16 of x[v] for v < 16, of x[v - 16] - f16(x[v - 16]) for v >= 16;
+//     perm8(j): the f16 of x[v] / s_v for v < 16, of the remainder of x[v - 16] / s_{v - 16}
+//     for v >= 16;
 //   unit 16, lane l < 32: element j = the hi (v < 16) or lo part of S[t][perm8(j)] / 32, the f32
-//     sum of sub-block perm8(j) of b; lanes >= 32 zero.
-// Tokens >= M are zero.
+//     sum of the scaled sub-block perm8(j) of b; lanes >= 32 zero.
+// Tokens >= M are zero (scale 1).
 constexpr int kUnitsSB = 17;
 
 // s_waitcnt immediate for vmcnt(n) with lgkmcnt(0); see q4k_gemm32.hip for the bare barrier.
@@ -58,6 +63,10 @@ constexpr int wait_vm16(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
     __builtin_amdgcn_s_barrier();    \
     asm volatile("" ::: "memory");   \
   } while (0)
+
+// 32-row MFMA tiles per wave: two for Q4_K, one for Q6_K (its records need more registers).
+template <int FMT>
+constexpr int tiles16() { return FMT == 0 ? 2 : 1; }
 
 // One super-block's weight data of a lane.
 // Q4_K (two 32-row MFMA tiles per wave): per tile the 16-byte header of the lane's row and the
@@ -92,7 +101,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int rb = blockIdx.x / SK, sp = blockIdx.x - rb * SK;
   const int kb0 = sp * nblk / SK, kb1 = (sp + 1) * nblk / SK;  // >= 1 super-block: SK <= nblk
   const int nb = kb1 - kb0;
-  constexpr int NT = FMT == 0 ? 2 : 1;           // 32-row MFMA tiles per wave
+  constexpr int NT = tiles16<FMT>();              // 32-row MFMA tiles per wave
   constexpr int TWG = 8 * NT;                      // 16-row tiles per workgroup
   constexpr int kRec = FMT == 0 ? kQ4kRecord : kQ6kRecord;
   constexpr int kWL = FMT == 0 ? 10 : 14;          // record loads per super-block per lane
@@ -145,7 +154,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int q = 0; q < 4; ++q)
       xv[q] = xvalid ? xrow[64 * (size_t)b + q] : float4{0.f, 0.f, 0.f, 0.f};
   };
-  auto store_x = [&](const float4 (&xv)[4], u32x4 *dst) {
+  // sk: the token's range scale exponent (0 for a range holding a NaN or an infinity: those
+  // values reach the token's own operand rows only, and so only its outputs)
+  auto store_x = [&](float4 (&xv)[4], u32x4 *dst, int sk) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      xv[q].x = ldexpf(xv[q].x, -sk);
+      xv[q].y = ldexpf(xv[q].y, -sk);
+      xv[q].z = ldexpf(xv[q].z, -sk);
+      xv[q].w = ldexpf(xv[q].w, -sk);
+    }
     const float f[16] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w,
                          xv[2].x, xv[2].y, xv[2].z, xv[2].w, xv[3].x, xv[3].y, xv[3].z, xv[3].w};
     float ps = 0.f;
@@ -195,14 +213,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   W16<FMT> wr[2];
   float4 xv[4];
-  load_x(kb0, xv);
+  // The first two super-blocks' records go out first, so they stream in while the range scale
+  // below is worked out.
   load_w(kb0, wr[0]);
   load_w(min(kb0 + 1, kb1 - 1), wr[1]);
+  // The token's largest magnitude over the K range, as the largest magnitude bit pattern (it
+  // orders like the magnitudes; a NaN or an infinity makes it >= 0x7F800000): each stage lane
+  // reads its 16 values of every super-block of the range, then the 16 lanes of the token
+  // (adjacent: tid = 16 xt + ...) reduce with xor-swizzles (bit-mask mode, no address registers).
+  uint32_t mb = 0;
+  for (int b = kb0; b < kb1; ++b) {
+    load_x(b, xv);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      mb = max(max(max(mb, __float_as_uint(xv[q].x) & 0x7FFFFFFFu),
+                   __float_as_uint(xv[q].y) & 0x7FFFFFFFu),
+               max(__float_as_uint(xv[q].z) & 0x7FFFFFFFu, __float_as_uint(xv[q].w) & 0x7FFFFFFFu));
+  }
+  mb = max(mb, (uint32_t)__builtin_amdgcn_ds_swizzle((int)mb, (1 << 10) | 0x1F));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_ds_swizzle((int)mb, (2 << 10) | 0x1F));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_ds_swizzle((int)mb, (4 << 10) | 0x1F));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_ds_swizzle((int)mb, (8 << 10) | 0x1F));
+  const bool xfinite = mb < 0x7F800000u;
+  int xe = 0;
+  (void)frexpf(__uint_as_float(mb), &xe);
+  const int xsk = xfinite ? xe - 14 : 0;  // the range maximum / 2^xsk is in [2^13, 2^14)
+  __shared__ float tscale[16];
+  if (xsb == 0 && xhalf == 0)
+    tscale[xt] = !xfinite ? __builtin_nanf("") : mb ? ldexpf(1.f, xsk) : 1.f;
+  load_x(kb0, xv);
   if (tid < 64) {  // lanes 32..63 of both S units: zero for the whole kernel
     const int k = tid & 31;
     (tid < 32 ? As0 : As1)[16 * 64 + 32 + k] = u32x4{0u, 0u, 0u, 0u};
   }
-  store_x(xv, As0);
+  store_x(xv, As0, xsk);
   FHIP_LDS_BARRIER16(wait_vm16(0));
 
   // Passes of two super-blocks (stage buffer and weight slot u are compile-time). Every pass
@@ -346,17 +390,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // work it would wait for the records of b + 1 too.)
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(wait_vm16(kWL));
-      store_x(xv, buf(u ^ 1));
+      store_x(xv, buf(u ^ 1), xsk);
       FHIP_LDS_BARRIER16(wait_vm16(kWL));
     }
   }
   // D layout: lane (kap, rho) holds column rho and operand rows 8 (e / 4) + 4 kap + e % 4:
   // e < 8 the hi rows of tokens 8 (e / 4) + 4 kap + e % 4, e + 8 the lo rows of the same tokens.
+  // hi + lo rows, times the token's scale (the loop's barriers made tscale visible)
   float v[NT][8];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[t][e] = acc[t][e] + acc[t][e + 8];
+    for (int e = 0; e < 8; ++e)
+      v[t][e] = (acc[t][e] + acc[t][e + 8]) * tscale[8 * (e >> 2) + 4 * kap + (e & 3)];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int row = 16 * tile_of(t) + (lane & 15);  // recomputed: not kept live in the loop
@@ -418,7 +464,7 @@ template <int FMT>
 int launch_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
   if (M < 1 || M > 16) return fail(FHIP_EINVAL, "gemv16: M=%d outside 1..16", M);
   const int nblk = K / 256, ntiles = q4k_tiles(N);
-  const int nrb = ceil_div(ntiles, FMT == 0 ? 16 : 8);
+  const int nrb = ceil_div(ntiles, 8 * tiles16<FMT>());
   const int SK = gemv16_splits(nblk);
   float *part = nullptr;
   if (SK > 1) {

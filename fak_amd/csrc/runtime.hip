@@ -189,12 +189,13 @@ int fhip_init(char *name, int namelen, int *arch, size_t *total_mem) {
   g_cus = prop.multiProcessorCount;
   g_lds = (int)prop.sharedMemPerBlock;
   // Tuning overrides are read here once, never per call. FAK_HIP_GEMV16_FROM only names a width
-  // the two small-M kernels can both take (2..5); anything else keeps the rule.
+  // from which the 5..16-token kernel can take every wider call (1..5); anything else keeps the
+  // rule.
   g_tuning.gemv_tw = env_knob("FAK_HIP_GEMV_TW");
   g_tuning.gemv_kw = env_knob("FAK_HIP_GEMV_KW");
   g_tuning.gemv_globalx = env_knob("FAK_HIP_GEMV_GLOBALX");
   const int from16 = env_knob("FAK_HIP_GEMV16_FROM");
-  g_tuning.gemv16_from = from16 >= 2 && from16 <= 5 ? from16 : 0;
+  g_tuning.gemv16_from = from16 >= 1 && from16 <= 5 ? from16 : 0;
   g_tuning.gemm32_form = env_knob("FAK_HIP_GEMM32_FORM");
   g_tuning.gemm32_sk = env_knob("FAK_HIP_GEMM32_SK");
   g_tuning.gemm32_nwb = env_knob("FAK_HIP_GEMM32_NWB");

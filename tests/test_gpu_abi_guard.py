@@ -23,7 +23,7 @@ def test_raw_bytes_pointer_is_refused(hip):
         rc = lib.fhip_q4k_matmul_f32(draw.ptr, dx.ptr, dy.ptr, out, in_, 1)
         assert rc == fakhip.EINVAL
         assert "not a tiled Q4_K weight" in fakhip.last_error()
-        # laid out in place, the same buffer is accepted (packed size == raw size here: 64 rows)
+        # laid out by fhip_q4k_repack, the same bytes are accepted
         with Dev(lib.fhip_q4k_packed_bytes(out, in_)) as dp:
             fakhip.call("fhip_q4k_repack", dp.ptr, draw.ptr, out, in_)
             fakhip.call("fhip_q4k_matmul_f32", dp.ptr, dx.ptr, dy.ptr, out, in_, 1)
@@ -35,7 +35,8 @@ def test_raw_bytes_pointer_is_refused(hip):
 def test_wrong_shape_and_format_are_refused(hip):
     lib = fakhip.load()
     out, in_ = 48, 1024
-    w = fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(out, in_, 3).ctypes.data, out, in_)
+    raw = synth.q4k_weights(out, in_, 3)  # kept alive across the upload's host read
+    w = fakhip.alloc_call("fhip_q4k_upload", raw.ctypes.data, out, in_)
     try:
         with Dev.from_host(synth.activations(2, 2048, 4)) as dx, Dev(2 * 2048 * 4) as dy:
             for o, i in [(out + 16, in_), (out, in_ + 256), (out - 1, in_)]:

@@ -21,10 +21,13 @@ def test_graph_replays_match_eager(hip):
     allocs, devs = [], []
     try:
         K = 1024
-        w1 = fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(1024, K, 11).ctypes.data, 1024, K)
-        wg = [fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(n, K, 12 + i).ctypes.data, n, K)
-              for i, n in enumerate((1024, 256, 256))]
-        w8 = fakhip.alloc_call("fhip_q8_0_upload", synth.q8_0_weights(512, K, 15).ctypes.data, 512, K)
+        r1 = synth.q4k_weights(1024, K, 11)  # host arrays stay alive across each upload
+        w1 = fakhip.alloc_call("fhip_q4k_upload", r1.ctypes.data, 1024, K)
+        rg = [synth.q4k_weights(n, K, 12 + i) for i, n in enumerate((1024, 256, 256))]
+        wg = [fakhip.alloc_call("fhip_q4k_upload", r.ctypes.data, r.size // (K // 256 * 144), K)
+              for r in rg]
+        r8 = synth.q8_0_weights(512, K, 15)
+        w8 = fakhip.alloc_call("fhip_q8_0_upload", r8.ctypes.data, 512, K)
         allocs += [w1, w8] + wg
         rng = np.random.default_rng(7)
         codes = Dev.from_host(rng.integers(-127, 128, 320 * K, dtype=np.int8))
@@ -56,9 +59,9 @@ def test_graph_replays_match_eager(hip):
             fakhip.call("fhip_q8_0_matmul_f32", w8, x1.ptr, outs["gguf"][k].ptr, 512, K, 1)
 
         def set_x(seed):
-            fakhip.call("fhip_h2d", x1.ptr, synth.activations(1, K, seed).ctypes.data, K * 4)
-            fakhip.call("fhip_h2d", x40.ptr, synth.activations(40, K, seed + 1).ctypes.data,
-                        40 * K * 4)
+            a1, a40 = synth.activations(1, K, seed), synth.activations(40, K, seed + 1)
+            fakhip.call("fhip_h2d", x1.ptr, a1.ctypes.data, K * 4)
+            fakhip.call("fhip_h2d", x40.ptr, a40.ctypes.data, 40 * K * 4)
 
         set_x(100)
         run(0)  # eager warm-up: sizes the workspace before capture
@@ -110,9 +113,11 @@ def test_graph_decode_ffn_replays(hip):
         H, I = 512, 2048  # K = 2048: the 8-token calls split K in two and reduce
         rng = np.random.default_rng(5)
         q6raw = qc.pin_d(rng.integers(0, 256, H * (I // 256) * 210, dtype=np.uint8), 0x1000)
-        g = fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(I, H, 31).ctypes.data, I, H)
-        u = fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(I, H, 32).ctypes.data, I, H)
-        d4 = fakhip.alloc_call("fhip_q4k_upload", synth.q4k_weights(H, I, 33).ctypes.data, H, I)
+        rgate, rup, rdown = (synth.q4k_weights(I, H, 31), synth.q4k_weights(I, H, 32),
+                             synth.q4k_weights(H, I, 33))  # alive across the uploads
+        g = fakhip.alloc_call("fhip_q4k_upload", rgate.ctypes.data, I, H)
+        u = fakhip.alloc_call("fhip_q4k_upload", rup.ctypes.data, I, H)
+        d4 = fakhip.alloc_call("fhip_q4k_upload", rdown.ctypes.data, H, I)
         d6 = fakhip.alloc_call("fhip_q6k_upload", q6raw.ctypes.data, H, I)
         allocs += [g, u, d4, d6]
         x3 = Dev(8 * H * 4)
@@ -135,9 +140,9 @@ def test_graph_decode_ffn_replays(hip):
             fakhip.call("fhip_q4k_matmul_f32", d4, xi.ptr, outs["q4v8"][k].ptr, H, I, 8)
 
         def set_x(seed):
-            fakhip.call("fhip_h2d", x3.ptr, synth.activations(8, H, seed).ctypes.data, 8 * H * 4)
-            fakhip.call("fhip_h2d", xi.ptr, synth.activations(20, I, seed + 1).ctypes.data,
-                        20 * I * 4)
+            a3, ai = synth.activations(8, H, seed), synth.activations(20, I, seed + 1)
+            fakhip.call("fhip_h2d", x3.ptr, a3.ctypes.data, 8 * H * 4)
+            fakhip.call("fhip_h2d", xi.ptr, ai.ctypes.data, 20 * I * 4)
 
         set_x(300)
         run(0)  # eager warm-up: sizes the workspace before capture

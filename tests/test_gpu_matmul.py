@@ -94,8 +94,19 @@ def test_q4k_gemv16_from_knob_is_clamped(hip, oracle_mod, monkeypatch):
     assert rel_err(Y, oracle_mod.q4k_gemm(raw, out, in_, X, P)) <= GEMV_TOL
 
 
+# The 1..4-token GEMV carries each activation as two int8 digits under a power-of-two scale per
+# 32 values, so every value keeps 2^-15 of its block's largest magnitude. When one activation
+# dominates a row's output (the 'outlier' rows: a lone 7e4 among N(0,1) values) its block-mates
+# are quantized coarsely relative to the output's scale: a numpy model of the digits gives
+# max|dY|/RMS 0.5-1.1e-3 on these rows, so that one case is held to 2e-3. Every other pattern,
+# and every pattern on the f16 routes (5..16 tokens: per-value hi/lo f16 under a power-of-two
+# super-block scale; the prefill GEMM: a power-of-two token scale), meets the route's bound.
+OUTLIER_INT8_TOL = 2e-3
+
+
 @pytest.mark.parametrize("pattern", ["big", "tiny", "mixed", "outlier"])
-@pytest.mark.parametrize("out,in_,P", [(1024, 3584, 1), (512, 2048, 4), (512, 2048, 64)])
+@pytest.mark.parametrize("out,in_,P", [(1024, 3584, 1), (512, 2048, 4), (512, 2048, 8),
+                                       (1024, 5120, 16), (512, 2048, 64)])
 def test_q4k_activation_scales(hip, oracle_mod, out, in_, P, pattern):
     """Activations far outside f16 (x 1e5, a lone 7e4), far below it (x 1e-20) and mixed within
     a row: every token row within its route's bound of the oracle, judged per row."""
@@ -107,7 +118,50 @@ def test_q4k_activation_scales(hip, oracle_mod, out, in_, P, pattern):
     ref = oracle_mod.q4k_gemm(raw, out, in_, X, P, workers=16)
     e = rel_err_rows(Y, ref)
     print(f"    per-row max|d|/RMS = {e:.3e}", flush=True)
-    assert e <= (GEMV_TOL if P <= 16 else GEMM_TOL), e
+    tol = GEMV_TOL if P <= 16 else GEMM_TOL
+    if pattern == "outlier" and P <= 4:
+        tol = OUTLIER_INT8_TOL
+    assert e <= tol, e
+
+
+@pytest.mark.parametrize("P", [8, 16])
+@pytest.mark.parametrize("out,in_", [(3584, 18944), (5120, 25600)])
+def test_q4k_verify_widths_large_activations(hip, oracle_mod, out, in_, P):
+    """The 5..16-token kernel on the down projections with rows of x 1e5, x 1e-20, mixed blocks
+    and a lone 7e4: the f16 operands never overflow or flush (full output checked)."""
+    from tests.gpu_util import rel_err_rows, scaled_activations
+    print(f"[case] q4k verify widths, large activations out={out} in={in_} P={P}", flush=True)
+    raw = synth.q4k_weights(out, in_, seed=out + 2 * P)
+    X = scaled_activations(P, in_, P + 3, "all")
+    Y = q4k_matmul(raw, out, in_, X, P)
+    e = rel_err_rows(Y, oracle_mod.q4k_gemm(raw, out, in_, X, P, workers=16))
+    print(f"    per-row max|d|/RMS = {e:.3e}", flush=True)
+    assert e <= GEMV_TOL, e
+
+
+def test_q4k_verify_matches_decode_argmax(hip, oracle_mod):
+    """Speculative verify runs 2..16 tokens through kernels whose arithmetic differs from the
+    one-token decode GEMV (int8 digits for 1..4 tokens, hi/lo f16 for 5..16), so a token's
+    output is not bit-identical across widths; the property verify needs is that greedy picks
+    agree. On the reference's CUDA witness weights (lcg 0x4b4b, randQ4KBytes) with every token's
+    activation aligned to a different row (alignActToRow, internal/compute/cuda_quant_test.go:
+    48-84, plus noise), each token's argmax at widths 2..16 equals its argmax decoded alone, and
+    the outputs agree within twice the GEMV bound."""
+    from tests import fixtures as fx
+    g = fx.LCG(0x4B4B)
+    out, in_ = 320, 256
+    raw = fx.rand_q4k_bytes(g, out, in_)
+    w = oracle_mod.q4k_dequant(raw, out, in_)
+    rng = np.random.default_rng(17)
+    targets = rng.choice(out, 16, replace=False)
+    X = np.stack([w[t] + 0.05 * rng.standard_normal(in_).astype(np.float32) * np.abs(w[t]).mean()
+                  for t in targets]).astype(np.float32)
+    Y1 = np.concatenate([q4k_matmul(raw, out, in_, X[t:t + 1], 1) for t in range(16)])
+    for k in (2, 3, 4, 5, 8, 16):
+        Yk = q4k_matmul(raw, out, in_, X[:k], k)
+        for t in range(k):
+            assert int(np.argmax(Yk[t])) == int(np.argmax(Y1[t])), (k, t)
+        assert rel_err(Yk, Y1[:k]) <= 2 * GEMV_TOL, k
 
 
 @pytest.mark.parametrize("pattern", ["big", "tiny", "mixed", "outlier", "all"])
