@@ -43,6 +43,10 @@ class ScratchScope {
   bool prev_on_;
 };
 
+// Resolves the device address of the no-allocation entry's static scratch on the current
+// device (noalloc.hip); called by fhip_init.
+int noalloc_setup();
+
 // Device properties cached by fhip_init.
 int cu_count();
 // Largest dynamic LDS allocation one workgroup may request (bytes).

@@ -188,6 +188,7 @@ int fhip_init(char *name, int namelen, int *arch, size_t *total_mem) {
                 prop.gcnArchName);
   g_cus = prop.multiProcessorCount;
   g_lds = (int)prop.sharedMemPerBlock;
+  if (int rc = noalloc_setup()) return rc;
   // Tuning overrides are read here once, never per call. FAK_HIP_GEMV16_FROM only names a width
   // from which the 5..16-token kernel can take every wider call (1..5); anything else keeps the
   // rule.

@@ -72,6 +72,7 @@ SIGNATURES = {
     "fhip_q8_0_matmul_f32": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "fhip_q4k_matmul_group_f32": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i]),
     "fhip_q4k_matmul_int8_f32": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "fhip_q4k_matmul_noalloc_f32": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "fhip_q6k_bytes": (C.c_size_t, [_i, _i]),
     "fhip_q6k_packed_bytes": (C.c_size_t, [_i, _i]),
     "fhip_q6k_repack": (_i, [_vp, _vp, _i, _i]),

@@ -147,6 +147,18 @@ int fhip_q4k_matmul_group_f32(const void *const *dPacked, float *const *dY, cons
 int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, float *dY, int out, int in,
                              int P);
 
+/* The same matmul for callers that cannot allocate device memory: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc. No counterpart in the
+ * reference. It runs the kernels of fhip_q4k_matmul_f32 (same results, bit for bit) but keeps
+ * their scratch (activation operands, token scales, K-range partial sums) in a static 64 MiB
+ * device array per device instead of the library workspace, and calls no hipMalloc / hipFree.
+ * A call whose scratch would exceed 64 MiB returns FHIP_EINVAL without launching anything
+ * (every GEMV of up to 16 tokens fits, and so does a prefill of 512 tokens at the 7B shapes; a
+ * prefill of 1,024 tokens through the 18944 -> 3584 projection does not). The array keeps the last call's contents and is shared by every call on the device: calls that
+ * overlap on one device (two streams, two threads) race on it. */
+int fhip_q4k_matmul_noalloc_f32(const void *dPacked, const float *dX, float *dY, int out, int in,
+                                int P);
+
 /* ---- Q6_K (256-weight super-blocks of 210 B; internal/model/quant_kquant.go:45,139-163) ---- */
 
 /* Bytes of a raw Q6_K weight [out][in] (in a multiple of 256); 0 for a bad shape. */

@@ -1,0 +1,61 @@
+"""fhip_q4k_matmul_noalloc_f32, the Q4_K matmul whose scratch is a static device array: it runs
+the kernels of fhip_q4k_matmul_f32, so its output must be the same bits, call after call, with
+the array keeping an earlier, larger call's contents; a call needing more scratch than the array
+holds is refused before anything is launched."""
+import numpy as np
+import pytest
+
+from fak_amd import fakhip, synth
+from tests.gpu_util import Dev, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def run(fn, w, X, out, in_, P):
+    with Dev.from_host(np.ascontiguousarray(X, np.float32)) as dx, Dev(P * out * 4) as dy:
+        fakhip.call(fn, w, dx.ptr, dy.ptr, out, in_, P)
+        return dy.to_host(np.float32).reshape(P, out)
+
+
+# (out, in, P): a K-split prefill GEMM (operands + token scales + partials: ~56 MB of scratch),
+# then smaller calls: a 16-token GEMV with K-range partials, a 3-token GEMV with global
+# activation operands, one decode token.
+CALLS = [(3584, 18944, 512), (2048, 6144, 16), (3584, 18944, 3), (1024, 3584, 1)]
+
+
+@pytest.mark.parametrize("first,second", [(0, 1), (1, 2), (2, 3), (0, 3)])
+def test_noalloc_matches_allocating_entry(hip, oracle_mod, first, second):
+    lib = fakhip.load()
+    for idx in (first, second):
+        out, in_, P = CALLS[idx]
+        print(f"[noalloc] out={out} in={in_} P={P}", flush=True)
+        raw = synth.q4k_weights(out, in_, seed=idx + 1)
+        X = synth.activations(P, in_, seed=idx + 11)
+        w = fakhip.alloc_call("fhip_q4k_upload", raw.ctypes.data, out, in_)
+        try:
+            a = run("fhip_q4k_matmul_noalloc_f32", w, X, out, in_, P)
+            b = run("fhip_q4k_matmul_f32", w, X, out, in_, P)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+            rows = np.arange(min(out, 64))
+            rb = (in_ // 256) * 144
+            sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in rows])
+            ref = oracle_mod.q4k_gemm(sub, len(rows), in_, X, P, workers=16)
+            assert rel_err(a[:, rows], ref) <= (1e-3 if P <= 16 else 1e-2)
+        finally:
+            lib.fhip_free(w)
+
+
+def test_noalloc_refuses_oversized_scratch(hip):
+    lib = fakhip.load()
+    out, in_, P = 3584, 18944, 1024  # prefill operands + partials > 64 MiB
+    raw = synth.q4k_weights(out, in_, 3)  # kept alive across the upload's host read
+    w = fakhip.alloc_call("fhip_q4k_upload", raw.ctypes.data, out, in_)
+    try:
+        with Dev(P * in_ * 4) as dx, Dev(P * out * 4) as dy:
+            assert lib.fhip_q4k_matmul_noalloc_f32(w, dx.ptr, dy.ptr, out, in_, P) == fakhip.EINVAL
+            assert "static region" in fakhip.last_error()
+            raw_ptr = dx.ptr
+            assert lib.fhip_q4k_matmul_noalloc_f32(raw_ptr, dx.ptr, dy.ptr, out, in_, 1) == \
+                fakhip.EINVAL
+    finally:
+        lib.fhip_free(w)
