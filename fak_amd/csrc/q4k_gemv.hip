@@ -537,16 +537,24 @@ I8Plan plan_i8(int ntiles, int K, bool swiglu) {
   const int nbp = (nblk + p.SK - 1) / p.SK;  // super-blocks per split (at most)
   const size_t ldsx = (size_t)nbp * op_bytes<MP>();
   i8_shape(ntiles, nblk / p.SK, max_waves, ldsx, (size_t)64 * NT * 4, p.TW, p.KW);
-  // One token over at most two tiles per CU: one 16-wave workgroup per CU (one tile, or two
-  // above one tile per CU), each wave streaming >= 1.5 records. More waves hide more of the
-  // record latency than longer per-wave streams do. Measured (us, this rule / the rule above):
-  // 3584 x 18944 13.2 / 13.8, 3584 x 3584 5.9 / 6.2, 4096 x 5120 7.2 / 8.6, 5120 x 5120 7.4 /
-  // 8.7, 4608 x 3584 6.6 / 7.2, 8192 x 5120 8.2 / 10.0, 5120 x 25600 21.7 / 22.1.
+  // At most two tiles per CU: one workgroup of max_waves waves per CU (one tile, or two above
+  // one tile per CU), each wave streaming >= 1.5 records; more waves hide more of the record
+  // latency than longer per-wave streams do. Two to four tokens over 2..8 tiles per CU: eight
+  // one-wave tiles per workgroup, which share the (larger) quantization. Measured (us, this rule
+  // / the rule above), one token: 3584 x 18944 13.2 / 13.8, 3584 x 3584 5.9 / 6.2, 4096 x 5120
+  // 7.2 / 8.6, 5120 x 5120 7.4 / 8.7, 4608 x 3584 6.6 / 7.2, 8192 x 5120 8.2 / 10.0, 5120 x
+  // 25600 21.7 / 22.1; four tokens: 3584 x 3584 8.0 / 8.6, 5120 x 5120 10.5 / 11.9, 18944 x
+  // 3584 14.5 / 16.2, 25600 x 5120 19.9 / 20.1.
   const int cus = cu_count() > 0 ? cu_count() : 256;
-  if (MP == 1 && !tuning().gemv_tw && !tuning().gemv_kw && ntiles <= 2 * cus) {
-    p.TW = ntiles <= cus ? 1 : 2;
-    p.KW = max_waves / p.TW;
-    while (p.KW > 1 && 2 * nblk < 3 * p.KW) p.KW /= 2;
+  if (!tuning().gemv_tw && !tuning().gemv_kw) {
+    if (ntiles <= 2 * cus) {
+      p.TW = ntiles <= cus ? 1 : 2;
+      p.KW = max_waves / p.TW;
+      while (p.KW > 1 && 2 * nblk < 3 * p.KW) p.KW /= 2;
+    } else if (MP > 1 && ntiles <= 8 * cus) {
+      p.TW = max_waves;
+      p.KW = 1;
+    }
   }
   if (p.KW > nblk / p.SK) p.KW = nblk / p.SK;
   if (swiglu && (p.TW & 1)) {  // both tiles of a row block in one workgroup
