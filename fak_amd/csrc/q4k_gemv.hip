@@ -25,19 +25,20 @@
 // Two tokens use two results (sub-blocks 0-3, 4-7), four tokens one result per chunk.
 //
 // Work split: a workgroup owns TW 16-row tiles, each worked by KW waves on contiguous parts of
-// the super-blocks. Every wave first puts its first PF weight records in flight, then the
-// whole workgroup quantizes the activations of all of K once into LDS for its TW tiles (when
-// that does not fit, gemv_i8_prep_kernel writes them to global memory once). Each wave streams
-// its tiled weight records (tiled.hpp) exactly once with three 16-byte loads per lane, keeping
-// PF in flight; the KW partials of a tile are summed through LDS in part order
-// (deterministic).
+// the super-blocks. The workgroup quantizes the activations of all of K once into LDS for its
+// TW tiles (when that does not fit, gemv_i8_prep_kernel writes them to global memory once).
+// Each wave streams its tiled weight records (tiled.hpp) exactly once with three 16-byte loads
+// per lane, keeping PF in flight; the KW partials of a tile are summed through LDS in part
+// order (deterministic).
 //
-// Split K across workgroups (SK > 1, for few tiles and long rows such as the 7B down
-// projection's 224 tiles x 74 super-blocks): workgroup (group of TW tiles, part p) covers
-// super-blocks [p nblk / SK, (p + 1) nblk / SK) and quantizes only those activations. Each
-// finished tile writes its partial to a global buffer, fences, and bumps the tile's counter; the
-// workgroup that arrives last sums the SK partials in part order (deterministic, whichever
-// arrives last), writes Y and resets the counter. Nothing waits on another workgroup.
+// Launch order. Vector loads complete in issue order per CU, and at the start of a launch every
+// CU puts a burst of weight records in flight (most of a 38 MB matrix when the grid is one
+// 16-wave workgroup per CU). Activation loads issued behind that burst land only when it has
+// drained, and the quantization, the barrier and the first MFMA with them. So when each wave
+// has at most kXPre (token, super-block) chunks to quantize, the kernel's first instructions
+// load them (coalesced: one 1 KB load per chunk), a bare barrier keeps every wave's records
+// behind every wave's activation loads, and the chunks are quantized lane-parallel
+// (quant_lanes) while the records stream in.
 //
 // SwiGLU mode (the first stage of the fused decode MLP): the group is {gate, up} with tiles
 // interleaved (gate tile T, up tile T, gate tile T + 1, ...) and TW even, so both tiles of a row
@@ -49,6 +50,11 @@ namespace fhip {
 namespace {
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ntload(const uint4 *p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 // ---- Activation operand layout for MP (1, 2, 4) token rows --------------------------------
 // Per super-block: MP result blocks of 16 rows x 4 lane groups x 16 bytes (entry index
@@ -90,13 +96,8 @@ template <int MP>
 __host__ __device__ constexpr size_t op_bytes() { return (size_t)MP * 1024 + (size_t)MP * 64; }
 
 
-// Quantize one 32-value sub-block of one token (zeros when !valid) into the layout above.
-// A: operand entries of super-block slot bl; ES: its {e, S} pairs.
-template <int MP>
-__device__ __forceinline__ void quant_block(const float *__restrict__ x, bool valid, int sig,
-                                            int t, uint4 *__restrict__ A,
-                                            float2 *__restrict__ ES) {
-  float v[32];
+// The 32 values of one sub-block of one token (zeros when !valid).
+__device__ __forceinline__ void load_block(const float *__restrict__ x, bool valid, float (&v)[32]) {
   if (valid) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -107,12 +108,30 @@ __device__ __forceinline__ void quant_block(const float *__restrict__ x, bool va
 #pragma unroll
     for (int i = 0; i < 32; ++i) v[i] = 0.f;
   }
-  float amax = 0.f, s = 0.f;
+}
+
+// S of a sub-block in a fixed pairwise order: quads p_k = (v0 + v1) + (v2 + v3) of values
+// 4k..4k+3, then ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)). quant_lanes computes the
+// same tree across eight lanes, so every path gives the same bits.
+__device__ __forceinline__ float quad_sum(float a, float b, float c, float d) {
+  return (a + b) + (c + d);
+}
+__device__ __forceinline__ float block_sum(const float (&v)[32]) {
+  float p[8];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    amax = fmaxf(amax, fabsf(v[i]));
-    s += v[i];
-  }
+  for (int k = 0; k < 8; ++k) p[k] = quad_sum(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+  return quad_sum(p[0], p[1], p[2], p[3]) + quad_sum(p[4], p[5], p[6], p[7]);
+}
+
+// Quantize the 32 values v of sub-block sig of token t into the layout above.
+// A: operand entries of super-block slot bl; ES: its {e, S} pairs.
+template <int MP>
+__device__ __forceinline__ void quant_vals(const float (&v)[32], int sig, int t,
+                                           uint4 *__restrict__ A, float2 *__restrict__ ES) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  const float s = block_sum(v);
   // e = 2^k, the smallest power of two with 127 e >= amax (amax = f 2^E, f in [0.5, 1)), so
   // x / e is exact and integer activations quantize without error. Non-finite blocks get
   // e = NaN, which carries into every output that uses them.
@@ -144,6 +163,58 @@ __device__ __forceinline__ void quant_block(const float *__restrict__ x, bool va
     row0[g] = (sig & 1) ? make_uint4(0, 0, a0, a1) : make_uint4(a0, a1, 0, 0);
     row1[g] = (sig & 1) ? make_uint4(0, 0, c0, c1) : make_uint4(c0, c1, 0, 0);
   }
+}
+
+// Quantize one 32-value sub-block of one token (zeros when !valid) into the layout above.
+template <int MP>
+__device__ __forceinline__ void quant_block(const float *__restrict__ x, bool valid, int sig,
+                                            int t, uint4 *__restrict__ A,
+                                            float2 *__restrict__ ES) {
+  float v[32];
+  load_block(x, valid, v);
+  quant_vals<MP>(v, sig, t, A, ES);
+}
+
+// Lane-parallel quantization of one super-block of one token, loaded coalesced: lane l holds
+// values 4 (l & 7) .. 4 (l & 7) + 3 of sub-block l >> 3 in v. Bit-identical to quant_vals: the
+// scale comes from the block maximum (order-free), each digit from its own value, and the
+// block sum is block_sum's tree, its levels taken across lanes (lane ^ 1, lane ^ 2, then the
+// other quad of the eight, each pair added in either order: the sum commutes exactly).
+#define FHIP_DPP(v, ctrl) \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, false))
+
+template <int MP>
+__device__ __forceinline__ void quant_lanes(const float4 v, int lane, int t,
+                                            uint4 *__restrict__ A, float2 *__restrict__ ES) {
+  const int sig = lane >> 3, p = lane & 7;
+  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  amax = fmaxf(amax, FHIP_DPP(amax, 0xB1));   // quad_perm [1,0,3,2]: lane ^ 1
+  amax = fmaxf(amax, FHIP_DPP(amax, 0x4E));   // quad_perm [2,3,0,1]: lane ^ 2
+  amax = fmaxf(amax, FHIP_DPP(amax, 0x141));  // row_half_mirror: the other quad of the eight
+  float sum = quad_sum(v.x, v.y, v.z, v.w);
+  sum = sum + FHIP_DPP(sum, 0xB1);
+  sum = sum + FHIP_DPP(sum, 0x4E);
+  sum = sum + FHIP_DPP(sum, 0x141);
+  int E;
+  const float f = frexpf(amax, &E);
+  const int k = E - 7 + (f > 127.f / 128.f ? 1 : 0);
+  float e = amax > 0.f ? ldexpf(1.f, k) : 0.f;
+  const float inv = amax > 0.f ? ldexpf(1.f, -k) : 0.f;
+  if (!(amax <= 3.4e38f)) e = __builtin_nanf("");
+  if (p == 0) ES[es_of<MP>(sig, t)] = make_float2(e, sum);
+  const float inv256 = inv * 256.f;
+  const int T0 = __float2int_rn(v.x * inv256), T1 = __float2int_rn(v.y * inv256);
+  const int T2 = __float2int_rn(v.z * inv256), T3 = __float2int_rn(v.w * inv256);
+  const uint32_t a = pack_byte(T0 + 128, T1 + 128, T2 + 128, T3 + 128, 1);
+  const uint32_t c = pack_byte(T0, T1, T2, T3, 0);
+  const int blk = blk_of<MP>(sig), g = p >> 1, half = p & 1;
+  uint32_t *row0 = reinterpret_cast<uint32_t *>(A + ((size_t)blk * 16 + row_of<MP>(sig, t, 0)) * 4 + g);
+  uint32_t *row1 = reinterpret_cast<uint32_t *>(A + ((size_t)blk * 16 + row_of<MP>(sig, t, 1)) * 4 + g);
+  const int dw = 2 * (sig & 1) + half, dz = 2 * ((sig & 1) ^ 1) + half;
+  row0[dw] = a;
+  row0[dz] = 0u;
+  row1[dw] = c;
+  row1[dz] = 0u;
 }
 
 // Quantize super-blocks [s0, s0 + nb) of M tokens (tokens M..MP-1 zero) into slots 0..nb-1 of
@@ -185,38 +256,76 @@ __device__ __forceinline__ float silu_f32(float z) {
   return z / (1.f + (float)exp(-(double)z));
 }
 
-// Per-tile arrival counters of the split-K reduction. Zero at load; every use returns its counter
-// to zero (the last arriver resets it), so calls and graph replays find them clear.
-constexpr int kMaxSplitTiles = 4096;
-__device__ unsigned g_split_cnt[kMaxSplitTiles];
-
 // Weight records each wave keeps in flight (LDS path) and the widest workgroup (waves) for one
 // token. Measured at the 7B FFN shapes: an 8-record ring with 8-wave workgroups, the
 // activation loads issued ahead of the ring, and lane-parallel coalesced quantization were all
 // slower (11.9-12 us gate/up, 14.7-15.1 us down, against 10.6 and 13.8 us here).
 constexpr int kPF1 = 4, kMaxWaves1 = 16;
+// Most super-blocks (of all tokens) a wave quantizes from activations loaded before its records.
+constexpr int kXPre = 8;
 
-template <int MP, bool LX, bool SWIGLU>
+// XM: how the activations reach LDS (LX only). kXLate: quant_range after the first records;
+// kXSpread: loaded first, chunk c by wave c % waves, one workgroup barrier before the records
+// are used; kXOwn (one tile per workgroup): each wave loads and quantizes the super-blocks of
+// its own K part, and no wave waits for another. PF0: records per wave put in flight before
+// the activations are quantized (kXSpread, kXOwn); the rest of the ring follows. A smaller first
+// burst lets the activations land sooner; a full one pays when every wave has several chunks.
+enum { kXLate = 0, kXSpread = 1, kXOwn = 2 };
+template <int MP, bool LX, bool SWIGLU, int XM, int PF0>
 __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_kernel(
     const GemvGroup grp, const float *__restrict__ X, const uint4 *__restrict__ xg, int K, int M,
-    int nblk, int TW, int KW, int SK, float *part_buf) {
+    int nblk, int TW, int KW) {
   constexpr int NT = MP == 1 ? 1 : 2;  // token slots per lane
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: SGPRs
+  const int nwaves = (int)(blockDim.x >> 6);
+
+  // First instructions: this wave's activation chunks (chunk c = token c / nblk, super-block
+  // c % nblk; see the launch order above), then the barrier that holds every record load
+  // behind every wave's activation loads.
+  const int nchunk = nblk * MP;
+  constexpr bool xpre = LX && XM != kXLate;
+  constexpr bool xown = LX && XM == kXOwn;
+  auto chunk_tok = [&](int c) {  // c / nblk without a division (MP <= 4)
+    return MP == 1 ? 0 : (c >= nblk) + (MP > 2 ? (c >= 2 * nblk) + (c >= 3 * nblk) : 0);
+  };
+  constexpr int kPT = kXPre / MP;  // super-blocks per token a kXOwn wave may hold
+  int ob0 = 0, onb = 0;  // kXOwn: this wave's K part (TW == 1, KW = waves)
+  if (xown) {
+    ob0 = wave * nblk / KW;
+    onb = (wave + 1) * nblk / KW - ob0;
+  }
+  float4 xv[kXPre];
+  if (xown) {
+#pragma unroll
+    for (int t = 0; t < MP; ++t)
+#pragma unroll
+      for (int i = 0; i < kPT; ++i)
+        if (i < onb)
+          xv[t * kPT + i] = *reinterpret_cast<const float4 *>(
+              X + (size_t)min(t, M - 1) * K + 256 * (size_t)(ob0 + i) + 4 * lane);
+  } else if (xpre) {
+#pragma unroll
+    for (int j = 0; j < kXPre; ++j) {
+      const int c = wave + j * nwaves;
+      if (c < nchunk) {
+        const int t = chunk_tok(c);
+        xv[j] = *reinterpret_cast<const float4 *>(X + (size_t)min(t, M - 1) * K +
+                                                  256 * (size_t)(c - t * nblk) + 4 * lane);
+      }
+    }
+  }
+  if (xpre) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  __builtin_amdgcn_sched_barrier(kNoVmemAcross);
+
   const int gq = lane >> 4, r = lane & 15;
   const int tile = wave / KW, part = wave - tile * KW;
-  // Tile group and K split of this workgroup, and its K range [kb0, kb1). Everything before
-  // the first weight loads delays the whole wave, so the unsplit case does no division here
-  // (and the products below stay in 32 bits: nblk * SK < 2^31).
-  int tgrp = blockIdx.x, sp = 0, kb0 = 0, kb1 = nblk;
-  if (SK > 1) {
-    tgrp = blockIdx.x / SK;
-    sp = blockIdx.x - tgrp * SK;
-    kb0 = sp * nblk / SK;
-    kb1 = (sp + 1) * nblk / SK;
-  }
-  const int Tg = tgrp * TW + tile;  // tile of the concatenated group
+  const int Tg = blockIdx.x * TW + tile;  // tile of the concatenated group
   const int ntiles = grp.tile0[grp.count];
   const bool tvalid = Tg < ntiles;
   int mem = 0;  // the member this tile belongs to (wave-uniform scalar search)
@@ -230,22 +339,18 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
   }
   const int N = grp.N[mem];
   float *__restrict__ Y = grp.Y[mem];
-  // This wave's part [b0, b1) of the workgroup's K range.
-  const int nbk = kb1 - kb0;
-  const int b0 = kb0 + part * nbk / KW;
-  const int b1 = kb0 + (part + 1) * nbk / KW;
-  const int nb = b1 - b0;  // super-blocks of this wave's K part (>= 1: KW <= nblk / SK)
+  // This wave's part [b0, b1) of the super-blocks.
+  const int b0 = part * nblk / KW;
+  const int b1 = (part + 1) * nblk / KW;
+  const int nb = b1 - b0;  // >= 1: KW <= nblk
   const uint8_t *base = grp.W[mem] + (size_t)T * nblk * kQ4kRecord;
 
-  // Operands of the workgroup's K range: in LDS (slot = super-block - kb0), quantized once by
-  // the whole workgroup for its TW tiles, or the prepared global buffer of all of K (slot =
-  // super-block). The LDS area holds ceil(nblk / SK) slots.
-  const int slot0 = LX ? kb0 : 0;
-  const int nslots = LX && SK > 1 ? (nblk + SK - 1) / SK : nblk;
+  // Operands: in LDS, quantized once by the whole workgroup for its TW tiles, or the prepared
+  // global buffer; slot = super-block either way.
   const unsigned char *opb = LX ? smem : reinterpret_cast<const unsigned char *>(xg);
   const uint4 *A = reinterpret_cast<const uint4 *>(opb);
-  const float2 *ES = reinterpret_cast<const float2 *>(opb + (size_t)nslots * MP * 1024);
-  float *red = reinterpret_cast<float *>(smem + (LX ? (size_t)nslots * op_bytes<MP>() : 0));
+  const float2 *ES = reinterpret_cast<const float2 *>(opb + (size_t)nblk * MP * 1024);
+  float *red = reinterpret_cast<float *>(smem + (LX ? (size_t)nblk * op_bytes<MP>() : 0));
 
   // A lane's operand row belongs to one chunk per result block; with one or two tokens the
   // lane loads only for the MFMA of that chunk.
@@ -271,17 +376,19 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
   };
   auto load = [&](int b, Ops &o) {
     const uint8_t *rec = base + (size_t)b * kQ4kRecord;
-    o.h = *reinterpret_cast<const uint4 *>(rec + 16 * r);
-    o.qa = *reinterpret_cast<const uint4 *>(rec + kQ4kHdr + 16 * lane);
-    o.qb = *reinterpret_cast<const uint4 *>(rec + kQ4kHdr + 1024 + 16 * lane);
+    // Every record is read once per call: non-temporal loads keep the weight stream from
+    // evicting what is reused from the L2 (the activations).
+    o.h = ntload(reinterpret_cast<const uint4 *>(rec + 16 * r));
+    o.qa = ntload(reinterpret_cast<const uint4 *>(rec + kQ4kHdr + 16 * lane));
+    o.qb = ntload(reinterpret_cast<const uint4 *>(rec + kQ4kHdr + 1024 + 16 * lane));
     if (!LX) {
 #pragma unroll
       for (int m = 0; m < 4; ++m)
         if (MP == 4 || lane_chunk(m * MP / 4) == m)
-          o.a[m] = __builtin_bit_cast(i32x4, A[a_index(b - slot0, m)]);
+          o.a[m] = __builtin_bit_cast(i32x4, A[a_index(b, m)]);
 #pragma unroll
       for (int blk = 0; blk < MP; ++blk)
-        o.es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b - slot0, blk)];
+        o.es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b, blk)];
     }
   };
 
@@ -292,13 +399,41 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
     if (!LX)
 #pragma unroll
       for (int m = 0; m < 4; ++m) ring[u].a[m] = i32x4{0, 0, 0, 0};
-    if (u < nb) load(b0 + u, ring[u]);
+    if (!xpre || u < PF0) load(min(b0 + u, b1 - 1), ring[u]);  // a repeat is never used
   }
   // With the first records in flight, the workgroup quantizes the activations of its K range.
   if (LX) {
-    quant_range<MP>(X, K, M, kb0, nbk, const_cast<uint4 *>(A), const_cast<float2 *>(ES),
-                    threadIdx.x, blockDim.x);
-    __syncthreads();
+    if (xown) {
+      // Only this wave reads these slots: LDS accesses of one wave complete in order, so no
+      // barrier is needed before its own reads.
+      const float4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < MP; ++t)
+#pragma unroll
+        for (int i = 0; i < kPT; ++i)
+          if (i < onb)
+            quant_lanes<MP>(t < M ? xv[t * kPT + i] : z, lane, t,
+                            const_cast<uint4 *>(A) + (size_t)(ob0 + i) * MP * 64,
+                            const_cast<float2 *>(ES) + (size_t)(ob0 + i) * 8 * MP);
+    } else if (xpre) {
+#pragma unroll
+      for (int j = 0; j < kXPre; ++j) {
+        const int c = wave + j * nwaves;
+        if (c < nchunk) {
+          const int t = chunk_tok(c), bl = c - t * nblk;
+          const float4 z = {0.f, 0.f, 0.f, 0.f};
+          quant_lanes<MP>(t < M ? xv[j] : z, lane, t, const_cast<uint4 *>(A) + (size_t)bl * MP * 64,
+                          const_cast<float2 *>(ES) + (size_t)bl * 8 * MP);
+        }
+      }
+    } else {
+      quant_range<MP>(X, K, M, 0, nblk, const_cast<uint4 *>(A), const_cast<float2 *>(ES),
+                      threadIdx.x, blockDim.x);
+    }
+    if (!xown) __syncthreads();
+    if (xpre)
+#pragma unroll
+      for (int u = PF0; u < PF; ++u) load(min(b0 + u, b1 - 1), ring[u]);
   }
   const uint32_t k0F = 0x0F0F0F0Fu;
 
@@ -327,10 +462,10 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
 #pragma unroll
         for (int m = 0; m < 4; ++m)
           if (MP == 4 || lane_chunk(m * MP / 4) == m)
-            areg[m] = __builtin_bit_cast(i32x4, A[a_index(b - slot0, m)]);
+            areg[m] = __builtin_bit_cast(i32x4, A[a_index(b, m)]);
 #pragma unroll
         for (int blk = 0; blk < MP; ++blk)
-          es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b - slot0, blk)];
+          es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b, blk)];
       } else {
 #pragma unroll
         for (int m = 0; m < 4; ++m) areg[m] = cur.a[m];
@@ -415,39 +550,6 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
     }
     return;
   }
-  if (!SWIGLU && SK > 1) {
-    // Split-K: publish this part, then the last of the SK workgroups of the tile reduces.
-    // The partials and the counter are accessed only through device-scope (sc1) stores, loads
-    // and atomics, which are coherent across the XCDs' L2s, so no cache-wide writeback or
-    // invalidate is needed: the writer waits for its partial stores to complete before it
-    // arrives, and the last arriver loads the partials only after its arrival returned.
-    const bool wr = row < N && gq < (MP == 4 ? 2 : 1);
-    if (wr)
-#pragma unroll
-      for (int s = 0; s < NT; ++s)
-        __hip_atomic_store(&part_buf[((size_t)sp * ntiles + Tg) * 64 + r * 4 + tok_of<MP>(gq, s)],
-                           v[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);  // every partial store acknowledged
-    unsigned old = 0;
-    if (lane == 0)
-      old = __hip_atomic_fetch_add(&g_split_cnt[Tg], 1u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-    old = __shfl(old, 0);
-    if (old != (unsigned)(SK - 1)) return;
-    if (lane == 0)
-      __hip_atomic_store(&g_split_cnt[Tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (wr)
-#pragma unroll
-      for (int s = 0; s < NT; ++s) {
-        const int t = tok_of<MP>(gq, s);
-        float a = 0.f;
-        for (int q = 0; q < SK; ++q)
-          a += __hip_atomic_load(&part_buf[((size_t)q * ntiles + Tg) * 64 + r * 4 + t],
-                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (t < M) Y[(size_t)t * N + row] = a;
-      }
-    return;
-  }
   if (row < N && gq < (MP == 4 ? 2 : 1)) {
 #pragma unroll
     for (int s = 0; s < NT; ++s) {
@@ -516,13 +618,14 @@ void i8_shape(int ntiles, int nblk, int max_waves, size_t lds_fixed, size_t lds_
   while (TW > 1 && TW * KW > max_waves) TW--;
 }
 
-// Launch shape of one small-M call: TW tiles x KW waves per workgroup, SK K-splits across
-// workgroups, activations in LDS or in a prepared global buffer, and the workspace it needs
-// (global operands, then the split-K partials).
+// Launch shape of one small-M call: TW tiles x KW waves per workgroup, activations in LDS or
+// in a prepared global buffer, and the workspace it needs (the global operands). K is not split
+// across workgroups: measured on the 7B and 27B down projections (partials combined through
+// device-scope stores and a per-tile arrival counter) it gained at most 5% and lost elsewhere.
 struct I8Plan {
-  int TW, KW, SK;
+  int TW, KW;
   bool lds_x;
-  size_t lds_bytes, xop_bytes, part_bytes;
+  size_t lds_bytes, xop_bytes;
 };
 
 template <int MP>
@@ -531,12 +634,8 @@ I8Plan plan_i8(int ntiles, int K, bool swiglu) {
   const int nblk = K / 256;
   const int max_waves = MP == 1 ? kMaxWaves1 : 8;
   I8Plan p{};
-  // No split of K across workgroups: measured on the 7B and 27B down projections it gained at
-  // most 5% and lost elsewhere.
-  p.SK = 1;
-  const int nbp = (nblk + p.SK - 1) / p.SK;  // super-blocks per split (at most)
-  const size_t ldsx = (size_t)nbp * op_bytes<MP>();
-  i8_shape(ntiles, nblk / p.SK, max_waves, ldsx, (size_t)64 * NT * 4, p.TW, p.KW);
+  const size_t ldsx = (size_t)nblk * op_bytes<MP>();
+  i8_shape(ntiles, nblk, max_waves, ldsx, (size_t)64 * NT * 4, p.TW, p.KW);
   // At most two tiles per CU: one workgroup of max_waves waves per CU (one tile, or two above
   // one tile per CU), each wave streaming >= 1.5 records; more waves hide more of the record
   // latency than longer per-wave streams do. Two to four tokens over 2..8 tiles per CU: eight
@@ -556,7 +655,7 @@ I8Plan plan_i8(int ntiles, int K, bool swiglu) {
       p.KW = 1;
     }
   }
-  if (p.KW > nblk / p.SK) p.KW = nblk / p.SK;
+  if (p.KW > nblk) p.KW = nblk;
   if (swiglu && (p.TW & 1)) {  // both tiles of a row block in one workgroup
     if (p.TW > 1) {
       p.TW -= 1;
@@ -570,24 +669,21 @@ I8Plan plan_i8(int ntiles, int K, bool swiglu) {
   p.lds_x = !tuning().gemv_globalx && ldsx + redB <= (size_t)lds_limit();
   p.lds_bytes = (p.lds_x ? ldsx : 0) + redB;
   p.xop_bytes = p.lds_x ? 0 : (((size_t)nblk * op_bytes<MP>() + 255) & ~(size_t)255);
-  p.part_bytes = p.SK > 1 ? (size_t)p.SK * ntiles * 64 * 4 : 0;
   return p;
 }
 
 // swiglu: the group is {gate, up} with tile0[2] = 2 * tiles (interleaved; see the kernel).
-// ws: a caller-provided workspace of plan_i8(...).xop_bytes + part_bytes (nullptr: the library
-// workspace).
+// ws: a caller-provided workspace of plan_i8(...).xop_bytes (nullptr: the library workspace).
 template <int MP>
 int launch_i8(const GemvGroup &g, const float *X, int K, int M, bool swiglu, void *ws) {
   const int nblk = K / 256, ntiles = g.tile0[g.count];
   const I8Plan p = plan_i8<MP>(ntiles, K, swiglu);
-  const size_t wsB = p.xop_bytes + p.part_bytes;
+  const size_t wsB = p.xop_bytes;
   if (!ws && wsB) ws = workspace(wsB);
   if (wsB && !ws) return FHIP_ENOMEM;
   if (int rc = check_disjoint("q4k_gemv", X, (size_t)M * K * 4, ws, wsB)) return rc;
   unsigned char *xop = (unsigned char *)ws;
-  float *part = p.part_bytes ? (float *)((unsigned char *)ws + p.xop_bytes) : nullptr;
-  const int grid = ceil_div(ntiles, p.TW) * p.SK, threads = 64 * p.TW * p.KW;
+  const int grid = ceil_div(ntiles, p.TW), threads = 64 * p.TW * p.KW;
   const uint4 *xg = nullptr;
   if (!p.lds_x) {
     const int nprep = MP * nblk * 8;
@@ -596,15 +692,34 @@ int launch_i8(const GemvGroup &g, const float *X, int K, int M, bool swiglu, voi
     FHIP_CHECK_LAUNCH("gemv_i8_prep_kernel");
     xg = (const uint4 *)xop;
   }
-#define FHIP_I8_LAUNCH(LXV, SWV)                                                             \
-  q4k_gemv_i8_kernel<MP, LXV, SWV><<<grid, threads, p.lds_bytes, stream()>>>(              \
-      g, X, xg, K, M, nblk, p.TW, p.KW, p.SK, part)
+#define FHIP_I8_LAUNCH(LXV, SWV, XMV, PF0V)                                                  \
+  q4k_gemv_i8_kernel<MP, LXV, SWV, XMV, PF0V><<<grid, threads, p.lds_bytes, stream()>>>(   \
+      g, X, xg, K, M, nblk, p.TW, p.KW)
+  // Activations loaded ahead of the records when each wave has at most kXPre chunks (kXOwn
+  // when each wave's own K part fits, one tile per workgroup). The full first burst for one
+  // token when every wave quantizes >= 3 chunks (the long-row down projections: 3584 x 18944
+  // 11.5 vs 11.8 us, 5120 x 25600 19.1 vs 19.6), else two records (18944 x 3584 10.5 vs 10.9,
+  // 3584 x 3584 5.1 vs 5.3, 5120 x 5120 7.3 vs 7.5).
+  const int nwaves = p.TW * p.KW;
+  const bool own = p.TW == 1 && ceil_div(nblk, p.KW) * MP <= kXPre;
+  const bool spread = nblk * MP <= kXPre * nwaves;
+  const bool full = MP == 1 && nblk >= 3 * nwaves;
   if (p.lds_x) {
-    if (swiglu) FHIP_I8_LAUNCH(true, true);
-    else FHIP_I8_LAUNCH(true, false);
+    if (swiglu) {
+      if (spread) FHIP_I8_LAUNCH(true, true, kXSpread, 2);
+      else FHIP_I8_LAUNCH(true, true, kXLate, 2);
+    } else if (own) {
+      if (full) FHIP_I8_LAUNCH(true, false, kXOwn, MP == 1 ? 4 : 2);
+      else FHIP_I8_LAUNCH(true, false, kXOwn, 2);
+    } else if (spread) {
+      if (full) FHIP_I8_LAUNCH(true, false, kXSpread, MP == 1 ? 4 : 2);
+      else FHIP_I8_LAUNCH(true, false, kXSpread, 2);
+    } else {
+      FHIP_I8_LAUNCH(true, false, kXLate, 2);
+    }
   } else {
-    if (swiglu) FHIP_I8_LAUNCH(false, true);
-    else FHIP_I8_LAUNCH(false, false);
+    if (swiglu) FHIP_I8_LAUNCH(false, true, kXLate, 2);
+    else FHIP_I8_LAUNCH(false, false, kXLate, 2);
   }
 #undef FHIP_I8_LAUNCH
   FHIP_CHECK_LAUNCH("q4k_gemv_i8_kernel");
@@ -639,7 +754,7 @@ size_t gemv_i8_ws_bytes(int ntiles, int K, int M, bool swiglu) {
   I8Plan p = M == 1 ? plan_i8<1>(ntiles, K, swiglu)
            : M == 2 ? plan_i8<2>(ntiles, K, swiglu)
                     : plan_i8<4>(ntiles, K, swiglu);
-  return p.xop_bytes + p.part_bytes;
+  return p.xop_bytes;
 }
 
 // Scratch bytes of a 1..16-token Q4_K matmul of an [N, K] weight (the route q4k_gemv takes).
