@@ -51,11 +51,6 @@ namespace {
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint4 ntload(const uint4 *p) {
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-
 // ---- Activation operand layout for MP (1, 2, 4) token rows --------------------------------
 // Per super-block: MP result blocks of 16 rows x 4 lane groups x 16 bytes (entry index
 // ((bl * MP + blk) * 16 + row) * 4 + g), then per (sub-block, token) a float2 {e, S}.
@@ -376,11 +371,9 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
   };
   auto load = [&](int b, Ops &o) {
     const uint8_t *rec = base + (size_t)b * kQ4kRecord;
-    // Every record is read once per call: non-temporal loads keep the weight stream from
-    // evicting what is reused from the L2 (the activations).
-    o.h = ntload(reinterpret_cast<const uint4 *>(rec + 16 * r));
-    o.qa = ntload(reinterpret_cast<const uint4 *>(rec + kQ4kHdr + 16 * lane));
-    o.qb = ntload(reinterpret_cast<const uint4 *>(rec + kQ4kHdr + 1024 + 16 * lane));
+    o.h = ld_stream(rec + 16 * r);
+    o.qa = ld_stream(rec + kQ4kHdr + 16 * lane);
+    o.qb = ld_stream(rec + kQ4kHdr + 1024 + 16 * lane);
     if (!LX) {
 #pragma unroll
       for (int m = 0; m < 4; ++m)

@@ -200,12 +200,12 @@ __global__ __launch_bounds__(512) void q6k_gemv_kernel(const uint8_t *__restrict
   };
   auto load = [&](int b, Rec &o) {
     const uint8_t *rec = base + (size_t)b * kQ6kRecord;
-    o.sc = *reinterpret_cast<const uint4 *>(rec + 16 * r);
-    o.dd = *reinterpret_cast<const uint32_t *>(rec + kQ6kD + 4 * (r >> 1));
-    o.ql0 = *reinterpret_cast<const uint4 *>(rec + kQ6kQl + 16 * lane);
-    o.ql1 = *reinterpret_cast<const uint4 *>(rec + kQ6kQl + 1024 + 16 * lane);
-    o.qh0 = *reinterpret_cast<const uint4 *>(rec + kQ6kQh + 256 * (gq & 1) + 16 * r);
-    o.qh1 = *reinterpret_cast<const uint4 *>(rec + kQ6kQh + 512 + 256 * (gq & 1) + 16 * r);
+    o.sc = ld_stream(rec + 16 * r);
+    o.dd = ld_stream32(rec + kQ6kD + 4 * (r >> 1));
+    o.ql0 = ld_stream(rec + kQ6kQl + 16 * lane);
+    o.ql1 = ld_stream(rec + kQ6kQl + 1024 + 16 * lane);
+    o.qh0 = ld_stream(rec + kQ6kQh + 256 * (gq & 1) + 16 * r);
+    o.qh1 = ld_stream(rec + kQ6kQh + 512 + 256 * (gq & 1) + 16 * r);
   };
   constexpr int PF = 4;
   Rec ring[PF];

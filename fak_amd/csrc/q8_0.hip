@@ -167,8 +167,8 @@ __global__ __launch_bounds__((LX && M <= 8) ? 1024 : 512) void q8_gemv_kernel(
   uint4 q = make_uint4(0, 0, 0, 0);
   if (p0 < p1) {
     const uint8_t *rec = base + (size_t)p0 * kQ8Record;
-    hd = *reinterpret_cast<const uint32_t *>(rec + 4 * r);
-    q = *reinterpret_cast<const uint4 *>(rec + kQ8Hdr + 16 * lane);
+    hd = ld_stream32(rec + 4 * r);
+    q = ld_stream(rec + kQ8Hdr + 16 * lane);
   }
   if (LX) {
     stage_x<M>(X, K, 0, ns, nsv, reinterpret_cast<uint4 *>(smem),
@@ -187,8 +187,8 @@ __global__ __launch_bounds__((LX && M <= 8) ? 1024 : 512) void q8_gemv_kernel(
     const uint4 qc = q;
     if (p + 1 < p1) {
       const uint8_t *rec = base + (size_t)(p + 1) * kQ8Record;
-      hd = *reinterpret_cast<const uint32_t *>(rec + 4 * r);
-      q = *reinterpret_cast<const uint4 *>(rec + kQ8Hdr + 16 * lane);
+      hd = ld_stream32(rec + 4 * r);
+      q = ld_stream(rec + kQ8Hdr + 16 * lane);
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
