@@ -118,6 +118,23 @@ __device__ __forceinline__ float block_sum(const float (&v)[32]) {
   return quad_sum(p[0], p[1], p[2], p[3]) + quad_sum(p[4], p[5], p[6], p[7]);
 }
 
+// Digits of four values x at scale 2^sh (|x| 2^sh <= 32512): y = x 2^sh + (1.5 2^23 + 128)
+// lies in [2^23, 2^24), where floats are the integers, so the add rounds x 2^sh half to even
+// exactly as rint and the low 23 bits of y hold 2^22 + T + 128. Byte 1 of y is then
+// q1 = (T + 128) >> 8 and byte 0 is the low byte of T + 128, i.e. q2 ^ 0x80. a gathers the
+// four q1, c the four q2 (value i in byte i).
+__device__ __forceinline__ void digits4(float x0, float x1, float x2, float x3, int sh,
+                                        uint32_t &a, uint32_t &c) {
+  constexpr float kMagic = 12583040.f;  // 1.5 * 2^23 + 128
+  const uint32_t y0 = __float_as_uint(ldexpf(x0, sh) + kMagic);
+  const uint32_t y1 = __float_as_uint(ldexpf(x1, sh) + kMagic);
+  const uint32_t y2 = __float_as_uint(ldexpf(x2, sh) + kMagic);
+  const uint32_t y3 = __float_as_uint(ldexpf(x3, sh) + kMagic);
+  a = __builtin_amdgcn_perm(y1, y0, 0x0C0C0501u) | __builtin_amdgcn_perm(y3, y2, 0x05010C0Cu);
+  c = (__builtin_amdgcn_perm(y1, y0, 0x0C0C0400u) | __builtin_amdgcn_perm(y3, y2, 0x04000C0Cu)) ^
+      0x80808080u;
+}
+
 // Quantize the 32 values v of sub-block sig of token t into the layout above.
 // A: operand entries of super-block slot bl; ES: its {e, S} pairs.
 template <int MP>
@@ -134,27 +151,22 @@ __device__ __forceinline__ void quant_vals(const float (&v)[32], int sig, int t,
   const float f = frexpf(amax, &E);
   const int k = E - 7 + (f > 127.f / 128.f ? 1 : 0);
   float e = amax > 0.f ? ldexpf(1.f, k) : 0.f;
-  const float inv = amax > 0.f ? ldexpf(1.f, -k) : 0.f;
   if (!(amax <= 3.4e38f)) e = __builtin_nanf("");
   ES[es_of<MP>(sig, t)] = make_float2(e, s);
 
   // T = rint(256 x / e), |T| <= 32512, so x ~= e T / 256 to within e / 512. The digits are
   // q1 = (T + 128) >> 8 (byte 1 of T + 128) and q2 = T - 256 q1 in [-128, 127] (the low byte
-  // of T), as two's complement bytes: q1 + q2 / 256 = T / 256 exactly. Each lane group's eight
-  // values are written as soon as they are packed.
-  const float inv256 = inv * 256.f;
+  // of T), as two's complement bytes: q1 + q2 / 256 = T / 256 exactly (digits4). Each lane
+  // group's eight values are written as soon as they are packed.
+  const int sh = 8 - k;
   const int blk = blk_of<MP>(sig);
   uint4 *row0 = A + ((size_t)blk * 16 + row_of<MP>(sig, t, 0)) * 4;
   uint4 *row1 = A + ((size_t)blk * 16 + row_of<MP>(sig, t, 1)) * 4;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    int T[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) T[i] = __float2int_rn(v[8 * g + i] * inv256);
-    const uint32_t a0 = pack_byte(T[0] + 128, T[1] + 128, T[2] + 128, T[3] + 128, 1);
-    const uint32_t a1 = pack_byte(T[4] + 128, T[5] + 128, T[6] + 128, T[7] + 128, 1);
-    const uint32_t c0 = pack_byte(T[0], T[1], T[2], T[3], 0);
-    const uint32_t c1 = pack_byte(T[4], T[5], T[6], T[7], 0);
+    uint32_t a0, a1, c0, c1;
+    digits4(v[8 * g], v[8 * g + 1], v[8 * g + 2], v[8 * g + 3], sh, a0, c0);
+    digits4(v[8 * g + 4], v[8 * g + 5], v[8 * g + 6], v[8 * g + 7], sh, a1, c1);
     row0[g] = (sig & 1) ? make_uint4(0, 0, a0, a1) : make_uint4(a0, a1, 0, 0);
     row1[g] = (sig & 1) ? make_uint4(0, 0, c0, c1) : make_uint4(c0, c1, 0, 0);
   }
@@ -194,14 +206,10 @@ __device__ __forceinline__ void quant_lanes(const float4 v, int lane, int t,
   const float f = frexpf(amax, &E);
   const int k = E - 7 + (f > 127.f / 128.f ? 1 : 0);
   float e = amax > 0.f ? ldexpf(1.f, k) : 0.f;
-  const float inv = amax > 0.f ? ldexpf(1.f, -k) : 0.f;
   if (!(amax <= 3.4e38f)) e = __builtin_nanf("");
   if (p == 0) ES[es_of<MP>(sig, t)] = make_float2(e, sum);
-  const float inv256 = inv * 256.f;
-  const int T0 = __float2int_rn(v.x * inv256), T1 = __float2int_rn(v.y * inv256);
-  const int T2 = __float2int_rn(v.z * inv256), T3 = __float2int_rn(v.w * inv256);
-  const uint32_t a = pack_byte(T0 + 128, T1 + 128, T2 + 128, T3 + 128, 1);
-  const uint32_t c = pack_byte(T0, T1, T2, T3, 0);
+  uint32_t a, c;
+  digits4(v.x, v.y, v.z, v.w, 8 - k, a, c);
   const int blk = blk_of<MP>(sig), g = p >> 1, half = p & 1;
   uint32_t *row0 = reinterpret_cast<uint32_t *>(A + ((size_t)blk * 16 + row_of<MP>(sig, t, 0)) * 4 + g);
   uint32_t *row1 = reinterpret_cast<uint32_t *>(A + ((size_t)blk * 16 + row_of<MP>(sig, t, 1)) * 4 + g);
