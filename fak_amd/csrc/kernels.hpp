@@ -89,12 +89,21 @@ __device__ __forceinline__ uint16_t ld_stream16(const void *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
 }
 
-// Byte k of each of a, b, c, d, packed into one word (a in byte 0).
-__device__ __forceinline__ uint32_t pack_byte(int a, int b, int c, int d, int k) {
-  const uint32_t lo = 0x0c0c0000u | (uint32_t)(4 + k) << 8 | (uint32_t)k;  // 0x0c selects 0
-  const uint32_t hi = (uint32_t)(4 + k) << 24 | (uint32_t)k << 16 | 0x0c0cu;
-  return __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, lo) |
-         __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, hi);
+// Two-digit int8 activations: the digits of four values x at scale 2^sh (|x| 2^sh <= 32512): y = x 2^sh + (1.5 2^23 + 128)
+// lies in [2^23, 2^24), where floats are the integers, so the add rounds x 2^sh half to even
+// exactly as rint and the low 23 bits of y hold 2^22 + T + 128. Byte 1 of y is then
+// q1 = (T + 128) >> 8 and byte 0 is the low byte of T + 128, i.e. q2 ^ 0x80. a gathers the
+// four q1, c the four q2 (value i in byte i).
+__device__ __forceinline__ void digits4(float x0, float x1, float x2, float x3, int sh,
+                                        uint32_t &a, uint32_t &c) {
+  constexpr float kMagic = 12583040.f;  // 1.5 * 2^23 + 128
+  const uint32_t y0 = __float_as_uint(ldexpf(x0, sh) + kMagic);
+  const uint32_t y1 = __float_as_uint(ldexpf(x1, sh) + kMagic);
+  const uint32_t y2 = __float_as_uint(ldexpf(x2, sh) + kMagic);
+  const uint32_t y3 = __float_as_uint(ldexpf(x3, sh) + kMagic);
+  a = __builtin_amdgcn_perm(y1, y0, 0x0C0C0501u) | __builtin_amdgcn_perm(y3, y2, 0x05010C0Cu);
+  c = (__builtin_amdgcn_perm(y1, y0, 0x0C0C0400u) | __builtin_amdgcn_perm(y3, y2, 0x04000C0Cu)) ^
+      0x80808080u;
 }
 
 // Workgroup shape of the small-M GEMV kernels (TW tiles x KW waves; see q4k_gemv.hip).

@@ -118,23 +118,6 @@ __device__ __forceinline__ float block_sum(const float (&v)[32]) {
   return quad_sum(p[0], p[1], p[2], p[3]) + quad_sum(p[4], p[5], p[6], p[7]);
 }
 
-// Digits of four values x at scale 2^sh (|x| 2^sh <= 32512): y = x 2^sh + (1.5 2^23 + 128)
-// lies in [2^23, 2^24), where floats are the integers, so the add rounds x 2^sh half to even
-// exactly as rint and the low 23 bits of y hold 2^22 + T + 128. Byte 1 of y is then
-// q1 = (T + 128) >> 8 and byte 0 is the low byte of T + 128, i.e. q2 ^ 0x80. a gathers the
-// four q1, c the four q2 (value i in byte i).
-__device__ __forceinline__ void digits4(float x0, float x1, float x2, float x3, int sh,
-                                        uint32_t &a, uint32_t &c) {
-  constexpr float kMagic = 12583040.f;  // 1.5 * 2^23 + 128
-  const uint32_t y0 = __float_as_uint(ldexpf(x0, sh) + kMagic);
-  const uint32_t y1 = __float_as_uint(ldexpf(x1, sh) + kMagic);
-  const uint32_t y2 = __float_as_uint(ldexpf(x2, sh) + kMagic);
-  const uint32_t y3 = __float_as_uint(ldexpf(x3, sh) + kMagic);
-  a = __builtin_amdgcn_perm(y1, y0, 0x0C0C0501u) | __builtin_amdgcn_perm(y3, y2, 0x05010C0Cu);
-  c = (__builtin_amdgcn_perm(y1, y0, 0x0C0C0400u) | __builtin_amdgcn_perm(y3, y2, 0x04000C0Cu)) ^
-      0x80808080u;
-}
-
 // Quantize the 32 values v of sub-block sig of token t into the layout above.
 // A: operand entries of super-block slot bl; ES: its {e, S} pairs.
 template <int MP>

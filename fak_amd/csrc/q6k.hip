@@ -144,22 +144,13 @@ __device__ __forceinline__ void q6_quant_group(const float *__restrict__ x, int 
   const float f = frexpf(amax, &E);
   const int k = E - 7 + (f > 127.f / 128.f ? 1 : 0);
   float e = amax > 0.f ? ldexpf(1.f, k) : 0.f;
-  const float inv = amax > 0.f ? ldexpf(1.f, -k) : 0.f;
   if (!(amax <= 3.4e38f)) e = __builtin_nanf("");
   reinterpret_cast<float2 *>(op + 512)[j] = make_float2(e, s);
-  const float inv256 = inv * 256.f;
-  int T[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) T[i] = __float2int_rn(v[i] * inv256);
   uint4 hi, lo;
-  hi.x = pack_byte(T[0] + 128, T[1] + 128, T[2] + 128, T[3] + 128, 1);
-  hi.y = pack_byte(T[4] + 128, T[5] + 128, T[6] + 128, T[7] + 128, 1);
-  hi.z = pack_byte(T[8] + 128, T[9] + 128, T[10] + 128, T[11] + 128, 1);
-  hi.w = pack_byte(T[12] + 128, T[13] + 128, T[14] + 128, T[15] + 128, 1);
-  lo.x = pack_byte(T[0], T[1], T[2], T[3], 0);
-  lo.y = pack_byte(T[4], T[5], T[6], T[7], 0);
-  lo.z = pack_byte(T[8], T[9], T[10], T[11], 0);
-  lo.w = pack_byte(T[12], T[13], T[14], T[15], 0);
+  digits4(v[0], v[1], v[2], v[3], 8 - k, hi.x, lo.x);
+  digits4(v[4], v[5], v[6], v[7], 8 - k, hi.y, lo.y);
+  digits4(v[8], v[9], v[10], v[11], 8 - k, hi.z, lo.z);
+  digits4(v[12], v[13], v[14], v[15], 8 - k, hi.w, lo.w);
   reinterpret_cast<uint4 *>(op)[2 * j] = hi;
   reinterpret_cast<uint4 *>(op)[2 * j + 1] = lo;
 }

@@ -33,9 +33,10 @@ def rel_err_rows(got: np.ndarray, ref: np.ndarray) -> float:
 
 def scaled_activations(P: int, K: int, seed: int, pattern: str) -> np.ndarray:
     """N(0,1) activations reshaped to stress the activation scaling of every route:
-    'big' rows x 1e5 (beyond f16), 'tiny' rows x 1e-20 (below f16), 'mixed' rows whose 32-value
-    blocks alternate x 1e4 / x 1e-20, 'outlier' rows with one value of 7e4 (>= 65504), and 'all'
-    cycling through the four by row."""
+    'big' rows x 1e5 (beyond f16), 'tiny' rows x 1e-20 (below f16), 'wee' rows x 1e-35 (block
+    maxima below 2^-113, where 2^8 / e overflows f32), 'mixed' rows whose 32-value blocks
+    alternate x 1e4 / x 1e-20, 'outlier' rows with one value of 7e4 (>= 65504), and 'all'
+    cycling through big, tiny, mixed and outlier by row."""
     rng = np.random.default_rng(seed)
     X = rng.standard_normal((P, K)).astype(np.float32)
     kinds = ["big", "tiny", "mixed", "outlier"] if pattern == "all" else [pattern]
@@ -45,6 +46,8 @@ def scaled_activations(P: int, K: int, seed: int, pattern: str) -> np.ndarray:
             X[t] *= np.float32(1e5)
         elif k == "tiny":
             X[t] *= np.float32(1e-20)
+        elif k == "wee":
+            X[t] *= np.float32(1e-35)
         elif k == "mixed":
             f = np.where((np.arange(K) // 32) % 2 == 0, 1e4, 1e-20).astype(np.float32)
             X[t] *= f

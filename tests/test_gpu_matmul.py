@@ -104,12 +104,12 @@ def test_q4k_gemv16_from_knob_is_clamped(hip, oracle_mod, monkeypatch):
 OUTLIER_INT8_TOL = 2e-3
 
 
-@pytest.mark.parametrize("pattern", ["big", "tiny", "mixed", "outlier"])
+@pytest.mark.parametrize("pattern", ["big", "tiny", "wee", "mixed", "outlier"])
 @pytest.mark.parametrize("out,in_,P", [(1024, 3584, 1), (512, 2048, 4), (512, 2048, 8),
                                        (1024, 5120, 16), (512, 2048, 64)])
 def test_q4k_activation_scales(hip, oracle_mod, out, in_, P, pattern):
-    """Activations far outside f16 (x 1e5, a lone 7e4), far below it (x 1e-20) and mixed within
-    a row: every token row within its route's bound of the oracle, judged per row."""
+    """Activations far outside f16 (x 1e5, a lone 7e4), far below it (x 1e-20, x 1e-35) and
+    mixed within a row: every token row within its route's bound of the oracle, judged per row."""
     from tests.gpu_util import rel_err_rows, scaled_activations
     print(f"[case] q4k scales out={out} in={in_} P={P} {pattern}", flush=True)
     raw = synth.q4k_weights(out, in_, seed=out + P)
