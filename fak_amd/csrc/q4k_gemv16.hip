@@ -149,20 +149,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const bool xvalid = xt < M;
   const float4 *xrow = reinterpret_cast<const float4 *>(X + (size_t)(xvalid ? xt : 0) * K +
                                                         32 * xsb + 16 * xhalf);
+  // Unconditional loads (tokens past M read token 0's row; store_x zeroes them): a load under
+  // the token test sits in an exec-masked branch, and the merge after it made the compiler wait
+  // for every load in flight, the records of the next super-block included.
   auto load_x = [&](int b, float4 (&xv)[4]) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      xv[q] = xvalid ? xrow[64 * (size_t)b + q] : float4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < 4; ++q) xv[q] = xrow[64 * (size_t)b + q];
   };
   // sk: the token's range scale exponent (0 for a range holding a NaN or an infinity: those
   // values reach the token's own operand rows only, and so only its outputs)
   auto store_x = [&](float4 (&xv)[4], u32x4 *dst, int sk) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      xv[q].x = ldexpf(xv[q].x, -sk);
-      xv[q].y = ldexpf(xv[q].y, -sk);
-      xv[q].z = ldexpf(xv[q].z, -sk);
-      xv[q].w = ldexpf(xv[q].w, -sk);
+      xv[q].x = xvalid ? ldexpf(xv[q].x, -sk) : 0.f;
+      xv[q].y = xvalid ? ldexpf(xv[q].y, -sk) : 0.f;
+      xv[q].z = xvalid ? ldexpf(xv[q].z, -sk) : 0.f;
+      xv[q].w = xvalid ? ldexpf(xv[q].w, -sk) : 0.f;
     }
     const float f[16] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w,
                          xv[2].x, xv[2].y, xv[2].z, xv[2].w, xv[3].x, xv[3].y, xv[3].z, xv[3].w};
@@ -213,22 +215,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   W16<FMT> wr[2];
   float4 xv[4];
-  // The first two super-blocks' records go out first, so they stream in while the range scale
-  // below is worked out.
+  auto absmax = [](uint32_t m, const float4 (&v)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      m = max(max(max(m, __float_as_uint(v[q].x) & 0x7FFFFFFFu),
+                  __float_as_uint(v[q].y) & 0x7FFFFFFFu),
+              max(__float_as_uint(v[q].z) & 0x7FFFFFFFu, __float_as_uint(v[q].w) & 0x7FFFFFFFu));
+    return m;
+  };
+  // Vector loads complete in issue order per CU: activation loads issued behind the first
+  // records land only when the records of every wave on the CU have. So a range of at most kPre
+  // super-blocks loads all its activations first (kept in registers for the range scale and the
+  // first stage), and a bare barrier holds every wave's records behind every wave's activation
+  // loads; longer ranges read them after the records.
+  constexpr int kPre = 5;
+  const bool xfirst = nb <= kPre;  // uniform over the workgroup
+  float4 xp[kPre][4];
+  if (xfirst) {
+    // Straight-line (a range shorter than kPre repeats its last super-block, which leaves the
+    // maximum unchanged), so the waits below count exactly.
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) load_x(kb0 + min(j, nb - 1), xp[j]);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // The first two super-blocks' records stream in while the range scale below is worked out.
   load_w(kb0, wr[0]);
   load_w(min(kb0 + 1, kb1 - 1), wr[1]);
+  if (xfirst) {
+    // Empty asm on the held activations: the range scale computed from them cannot be hoisted
+    // above the record loads (it would wait for the activations before any record went out).
+#pragma unroll
+    for (int j = 0; j < kPre; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) asm volatile("" : "+v"(xp[j][q].x), "+v"(xp[j][q].y), "+v"(xp[j][q].z), "+v"(xp[j][q].w));
+  }
   // The token's largest magnitude over the K range, as the largest magnitude bit pattern (it
   // orders like the magnitudes; a NaN or an infinity makes it >= 0x7F800000): each stage lane
   // reads its 16 values of every super-block of the range, then the 16 lanes of the token
   // (adjacent: tid = 16 xt + ...) reduce with xor-swizzles (bit-mask mode, no address registers).
   uint32_t mb = 0;
-  for (int b = kb0; b < kb1; ++b) {
-    load_x(b, xv);
+  if (xfirst) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      mb = max(max(max(mb, __float_as_uint(xv[q].x) & 0x7FFFFFFFu),
-                   __float_as_uint(xv[q].y) & 0x7FFFFFFFu),
-               max(__float_as_uint(xv[q].z) & 0x7FFFFFFFu, __float_as_uint(xv[q].w) & 0x7FFFFFFFu));
+    for (int j = 0; j < kPre; ++j) mb = absmax(mb, xp[j]);
+  } else {
+    for (int b = kb0; b < kb1; ++b) {
+      load_x(b, xv);
+      mb = absmax(mb, xv);
+    }
   }
   mb = max(mb, (uint32_t)__builtin_amdgcn_ds_swizzle((int)mb, (1 << 10) | 0x1F));
   mb = max(mb, (uint32_t)__builtin_amdgcn_ds_swizzle((int)mb, (2 << 10) | 0x1F));
@@ -241,13 +277,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ float tscale[16];
   if (xsb == 0 && xhalf == 0)
     tscale[xt] = !xfinite ? __builtin_nanf("") : mb ? ldexpf(1.f, xsk) : 1.f;
-  load_x(kb0, xv);
+  if (xfirst) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xv[q] = xp[0][q];
+  } else {
+    load_x(kb0, xv);
+  }
   if (tid < 64) {  // lanes 32..63 of both S units: zero for the whole kernel
     const int k = tid & 31;
     (tid < 32 ? As0 : As1)[16 * 64 + 32 + k] = u32x4{0u, 0u, 0u, 0u};
   }
   store_x(xv, As0, xsk);
-  FHIP_LDS_BARRIER16(wait_vm16(0));
+  // The first stage is in LDS; the first two super-blocks' records (2 kWL loads per lane) may
+  // still be in flight: the first pass waits for its own.
+  if (xfirst)
+    FHIP_LDS_BARRIER16(wait_vm16(2 * kWL));
+  else
+    FHIP_LDS_BARRIER16(wait_vm16(0));
 
   // Passes of two super-blocks (stage buffer and weight slot u are compile-time). Every pass
   // issues the same loads (indices clamped) and reaches the same barrier; a pass past the end of
