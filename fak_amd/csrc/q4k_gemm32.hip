@@ -206,6 +206,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   constexpr int kRec = F::kRec, kWU = F::kWU, kWPT = F::kWPT, kWUP = F::kWUP;
   __shared__ u32x4 As[2][kAU];
   __shared__ u32x4 Ws[NWB][kWUP];
+  __shared__ __align__(16) float ts_lds[kBM];  // the token scales of this token tile
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
@@ -269,6 +270,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   u32x4 areg[4], wreg[kWPT];
   LOAD_W(0, wreg)
   LOAD_A(0, areg)
+  if (tid < kBM) ts_lds[tid] = tscale[kBM * mg + tid];  // tscale holds MTG * kBM entries
   STORE_W(0, wreg)
 #pragma unroll
   for (int k = 0; k < 4; ++k) As[0][tid + 256 * k] = areg[k];
@@ -375,9 +377,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 #undef STORE_W
 
   // D layout: lane (kap, rho) holds column rho (the row o) and tokens 8 (v / 4) + 4 kap + v % 4.
+  // The token scales come from LDS, four per read: a global load per output would make every
+  // store wait for the previous one.
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int t0 = kBM * mg + 32 * (2 * wm + i) + 4 * kap;
+    const int tl0 = 32 * (2 * wm + i) + 4 * kap, t0 = kBM * mg + tl0;
+    float sc[16];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const float4 s4 = *reinterpret_cast<const float4 *>(ts_lds + tl0 + 8 * a);
+      sc[4 * a] = s4.x; sc[4 * a + 1] = s4.y; sc[4 * a + 2] = s4.z; sc[4 * a + 3] = s4.w;
+    }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int o = 16 * (kBT * ng + 4 * wn + 2 * t) + rho;
@@ -385,7 +395,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int tok = t0 + 8 * (v >> 2) + (v & 3);
-        if (tok < M) Y[(size_t)tok * N + o] = acc[i][t][v] * tscale[tok];
+        if (tok < M) Y[(size_t)tok * N + o] = acc[i][t][v] * sc[v];
       }
     }
   }
@@ -440,6 +450,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
   __shared__ u32x4 As2[kSU];
   __shared__ u32x4 As3[kSU];
   __shared__ u32x4 Ws[kWPT * kThreads];  // past kWU: padding (a repeat of unit 0)
+  __shared__ __align__(16) float ts_lds[kBM];  // the token scales of this token tile
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kap = lane >> 5, rho = lane & 31;
@@ -488,6 +499,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
   load_stage(0, As0);
   load_stage(1, As1);
   load_stage(2, As2);
+  for (int k = tid; k < kBM; k += kThreads) ts_lds[k] = tscale[kBM * mg + k];  // MTG * kBM entries
 #pragma unroll
   for (int k = 0; k < kWPT; ++k) Ws[tid + kThreads * k] = wreg[k];
   FHIP_LDS_BARRIER(wait_vm(0));
@@ -554,9 +566,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
   __builtin_amdgcn_s_waitcnt(wait_vm(0));  // no LDS DMA may be pending when the workgroup ends
 
   // D layout: lane (kap, rho) holds column rho (the row o) and tokens 8 (v / 4) + 4 kap + v % 4.
+  // The token scales come from LDS, four per read: a global load per output would make every
+  // store wait for the previous one.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int t0 = kBM * mg + 32 * i + 4 * kap;
+    const int tl0 = 32 * i + 4 * kap, t0 = kBM * mg + tl0;
+    float sc[16];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const float4 s4 = *reinterpret_cast<const float4 *>(ts_lds + tl0 + 8 * a);
+      sc[4 * a] = s4.x; sc[4 * a + 1] = s4.y; sc[4 * a + 2] = s4.z; sc[4 * a + 3] = s4.w;
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int o = 16 * (kBT * ng + (8 / NW) * wave + 2 * t) + rho;
@@ -565,7 +585,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
       for (int v = 0; v < 16; ++v) {
         const int tok = t0 + 8 * (v >> 2) + (v & 3);
         if (tok >= M) continue;
-        const float val = acc[i][t][v] * tscale[tok];
+        const float val = acc[i][t][v] * sc[v];
         if (SK == 1)
           Y[(size_t)tok * N + o] = val;
         else
