@@ -366,10 +366,10 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
     o.qa = ld_stream(rec + kQ4kHdr + 16 * lane);
     o.qb = ld_stream(rec + kQ4kHdr + 1024 + 16 * lane);
     if (!LX) {
+      // Every lane loads all four (an exec-masked load made the compiler wait for the whole
+      // ring after it); the lanes that do not own a chunk zero it at use.
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
-        if (MP == 4 || lane_chunk(m * MP / 4) == m)
-          o.a[m] = __builtin_bit_cast(i32x4, A[a_index(b, m)]);
+      for (int m = 0; m < 4; ++m) o.a[m] = __builtin_bit_cast(i32x4, A[a_index(b, m)]);
 #pragma unroll
       for (int blk = 0; blk < MP; ++blk)
         o.es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b, blk)];
@@ -439,6 +439,7 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
       // This slot's three loads are older than the other slots' refills: saying so lets the
       // compiler wait for just this record instead of draining the ring at the top of a pass.
       if (LX) __builtin_amdgcn_s_waitcnt(0x0F70 | (3 * (PF - 1)));
+      else __builtin_amdgcn_s_waitcnt(0x0F70 | ((7 + MP) * (PF - 1)));  // < 16 loads: PF = 2
       Ops &cur = ring[u];
 
       float4 es[MP];
@@ -452,7 +453,8 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
           es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b, blk)];
       } else {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) areg[m] = cur.a[m];
+        for (int m = 0; m < 4; ++m)
+          areg[m] = MP == 4 || lane_chunk(m * MP / 4) == m ? cur.a[m] : i32x4{0, 0, 0, 0};
 #pragma unroll
         for (int blk = 0; blk < MP; ++blk) es[blk] = cur.es[blk];
       }
