@@ -136,7 +136,9 @@ __global__ void q8_dequant_kernel(float *__restrict__ dw, const uint8_t *__restr
 
 __device__ __forceinline__ uint32_t b02(uint32_t q) { return (q & 0x00FF00FFu) | 0x64006400u; }
 
-template <int M, bool LX>
+// PF: records each wave keeps in flight (8 when its K part is long enough, else 2: a short part
+// would fill the ring with repeats of its last record).
+template <int M, bool LX, int PF>
 __global__ __launch_bounds__((LX && M <= 8) ? 1024 : 512) void q8_gemv_kernel(
     const uint8_t *__restrict__ W, const float *__restrict__ X, const uint4 *__restrict__ xg,
     float *__restrict__ Y, int N, int K, int npairs, int ntiles, int TW, int KW) {
@@ -163,18 +165,24 @@ __global__ __launch_bounds__((LX && M <= 8) ? 1024 : 512) void q8_gemv_kernel(
   }
   float *red = reinterpret_cast<float *>(smem + (LX ? xop_bytes(M, ns) : 0));
 
-  uint32_t hd = 0;
-  uint4 q = make_uint4(0, 0, 0, 0);
-  if (p0 < p1) {
-    const uint8_t *rec = base + (size_t)p0 * kQ8Record;
-    hd = ld_stream32(rec + 4 * r);
-    q = ld_stream(rec + kQ8Hdr + 16 * lane);
-  }
+  // The activations are staged first (vector loads complete in issue order per CU: behind a
+  // burst of records they would land only once the burst had), then each wave keeps PF records
+  // (two loads per lane each) in flight.
   if (LX) {
     stage_x<M>(X, K, 0, ns, nsv, reinterpret_cast<uint4 *>(smem),
                reinterpret_cast<float2 *>(smem + xop_a_bytes(M, ns)), threadIdx.x, blockDim.x);
     __syncthreads();
   }
+  uint32_t hdr[PF];
+  uint4 qr[PF];
+  auto load = [&](int p, int u) {
+    const uint8_t *rec = base + (size_t)p * kQ8Record;
+    hdr[u] = ld_stream32(rec + 4 * r);
+    qr[u] = ld_stream(rec + kQ8Hdr + 16 * lane);
+  };
+  if (p0 < p1)  // uniform; a part shorter than PF repeats its last record (never used)
+#pragma unroll
+    for (int u = 0; u < PF; ++u) load(min(p0 + u, p1 - 1), u);
 
   float acc[NSET][J];
 #pragma unroll
@@ -182,14 +190,16 @@ __global__ __launch_bounds__((LX && M <= 8) ? 1024 : 512) void q8_gemv_kernel(
 #pragma unroll
     for (int jj = 0; jj < J; ++jj) acc[k][jj] = 0.f;
 
-  for (int p = p0; p < p1; ++p) {
-    const uint32_t hc = hd;
-    const uint4 qc = q;
-    if (p + 1 < p1) {
-      const uint8_t *rec = base + (size_t)(p + 1) * kQ8Record;
-      hd = ld_stream32(rec + 4 * r);
-      q = ld_stream(rec + kQ8Hdr + 16 * lane);
-    }
+  for (int pp = p0; pp < p1; pp += PF)
+#pragma unroll
+  for (int u = 0; u < PF; ++u) {
+    const int p = pp + u;
+    if (p >= p1) break;
+    // This slot's two loads are older than the other slots': the wait leaves those in flight.
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * (PF - 1)));
+    const uint32_t hc = hdr[u];
+    const uint4 qc = qr[u];
+    load(min(p + PF, p1 - 1), u);  // unconditional (a repeat at the end is never used): exact waits
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int sl = 2 * p + h;
@@ -201,16 +211,19 @@ __global__ __launch_bounds__((LX && M <= 8) ? 1024 : 512) void q8_gemv_kernel(
       const bool sv = LX || sl < nsv;
 #pragma unroll
       for (int k = 0; k < NSET; ++k) {
+        // Unconditional loads at clamped indices, the unused values zeroed after: a load under
+        // a lane test made the compiler wait for every load in flight after it.
         const int rho = r + 16 * k;
         const bool have = rho < R2 && (LX || sl < nsv);
-        const f16x8 a = have ? __builtin_bit_cast(f16x8, A[(sl * 4 + g) * R2 + rho]) : f16x8{};
+        const f16x8 araw = __builtin_bit_cast(f16x8, A[(sl * 4 + g) * R2 + min(rho, R2 - 1)]);
+        const f16x8 a = have ? araw : f16x8{};
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
         const f32x4 dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bw, z, 0, 0, 0);
 #pragma unroll
         for (int jj = 0; jj < J; ++jj) {
           const int t = 8 * k + 2 * g + jj;
-          const float2 se = (t < M && sv) ? Ex[(sl >> 3) * M * 8 + t * 8 + (sl & 7)]
-                                          : make_float2(0.f, 0.f);
+          const float2 seraw = Ex[(sl >> 3) * M * 8 + min(t, M - 1) * 8 + (sl & 7)];
+          const float2 se = (t < M && sv) ? seraw : make_float2(0.f, 0.f);
           acc[k][jj] = fmaf(d * se.y, fmaf(-1152.f, se.x, dd[2 * jj] + dd[2 * jj + 1]), acc[k][jj]);
         }
       }
@@ -273,8 +286,15 @@ int launch_q8(const uint8_t *W, const float *X, float *Y, int N, int K) {
   const int grid = ceil_div(ntiles, TW), threads = 64 * TW * KW;
   const size_t redB = KW > 1 ? (size_t)TW * KW * 64 * VALS * 4 : 0;
   if (lds_x) {
-    q8_gemv_kernel<M, true><<<grid, threads, stage + redB, stream()>>>(W, X, nullptr, Y, N, K,
-                                                                       npairs, ntiles, TW, KW);
+    // Measured (us, ring of 8 / ring of 1 before): 18944 x 3584 one token 21.6 / 23.2, 3584 x
+    // 18944 four tokens 53.1 / 57.1; a 1536 x 576 matrix (about two records per wave) is
+    // faster with the short ring.
+    if (npairs >= 8 * KW)
+      q8_gemv_kernel<M, true, 8><<<grid, threads, stage + redB, stream()>>>(W, X, nullptr, Y, N, K,
+                                                                            npairs, ntiles, TW, KW);
+    else
+      q8_gemv_kernel<M, true, 2><<<grid, threads, stage + redB, stream()>>>(W, X, nullptr, Y, N, K,
+                                                                            npairs, ntiles, TW, KW);
     FHIP_CHECK_LAUNCH("q8_gemv_kernel<lds>");
     return FHIP_OK;
   }
@@ -284,8 +304,8 @@ int launch_q8(const uint8_t *W, const float *X, float *Y, int N, int K) {
   q8_xprep_kernel<M><<<ceil_div(ns * M, 128), 128, 0, stream()>>>(X, K, ns, K / 32,
                                                                    (uint4 *)xop);
   FHIP_CHECK_LAUNCH("q8_xprep_kernel");
-  q8_gemv_kernel<M, false><<<grid, threads, redB, stream()>>>(W, X, (const uint4 *)xop, Y, N, K,
-                                                              npairs, ntiles, TW, KW);
+  q8_gemv_kernel<M, false, 2><<<grid, threads, redB, stream()>>>(W, X, (const uint4 *)xop, Y, N,
+                                                                 K, npairs, ntiles, TW, KW);
   FHIP_CHECK_LAUNCH("q8_gemv_kernel<global>");
   return FHIP_OK;
 }
