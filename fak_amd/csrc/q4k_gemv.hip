@@ -256,8 +256,10 @@ constexpr int kXPre = 8;
 // its own K part, and no wave waits for another. PF0: records per wave put in flight before
 // the activations are quantized (kXSpread, kXOwn); the rest of the ring follows. A smaller first
 // burst lets the activations land sooner; a full one pays when every wave has several chunks.
+// EX: each ring slot is refilled unconditionally (the repeat of the last record at the end of a
+// part is never used), so every ring wait counts exactly; else only while records remain.
 enum { kXLate = 0, kXSpread = 1, kXOwn = 2 };
-template <int MP, bool LX, bool SWIGLU, int XM, int PF0>
+template <int MP, bool LX, bool SWIGLU, int XM, int PF0, bool EX>
 __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_kernel(
     const GemvGroup grp, const float *__restrict__ X, const uint4 *__restrict__ xg, int K, int M,
     int nblk, int TW, int KW) {
@@ -476,7 +478,10 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
       // The slot is refilled with the record PF ahead as soon as its operands are consumed;
       // the header words are kept for the scaling below.
       const uint4 h = cur.h;
-      if (b + PF < b1) load(b + PF, cur);
+      if (EX)
+        load(min(b + PF, b1 - 1), cur);
+      else if (b + PF < b1)
+        load(b + PF, cur);
 
       const float dd = (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xffffu));
       const float dmn = (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16));
@@ -678,9 +683,14 @@ int launch_i8(const GemvGroup &g, const float *X, int K, int M, bool swiglu, voi
     FHIP_CHECK_LAUNCH("gemv_i8_prep_kernel");
     xg = (const uint4 *)xop;
   }
-#define FHIP_I8_LAUNCH(LXV, SWV, XMV, PF0V)                                                  \
-  q4k_gemv_i8_kernel<MP, LXV, SWV, XMV, PF0V><<<grid, threads, p.lds_bytes, stream()>>>(   \
+#define FHIP_I8_LAUNCH_EX(LXV, SWV, XMV, PF0V, EXV)                                          \
+  q4k_gemv_i8_kernel<MP, LXV, SWV, XMV, PF0V, EXV><<<grid, threads, p.lds_bytes, stream()>>>( \
       g, X, xg, K, M, nblk, p.TW, p.KW)
+#define FHIP_I8_LAUNCH(LXV, SWV, XMV, PF0V)                                                  \
+  do {                                                                                       \
+    if (exact) FHIP_I8_LAUNCH_EX(LXV, SWV, XMV, PF0V, (MP > 1));                             \
+    else FHIP_I8_LAUNCH_EX(LXV, SWV, XMV, PF0V, false);                                      \
+  } while (0)
   // Activations loaded ahead of the records when each wave has at most kXPre chunks (kXOwn
   // when each wave's own K part fits, one tile per workgroup). The full first burst for one
   // token when every wave quantizes >= 3 chunks (the long-row down projections: 3584 x 18944
@@ -690,6 +700,13 @@ int launch_i8(const GemvGroup &g, const float *X, int K, int M, bool swiglu, voi
   const bool own = p.TW == 1 && ceil_div(nblk, p.KW) * MP <= kXPre;
   const bool spread = nblk * MP <= kXPre * nwaves;
   const bool full = MP == 1 && nblk >= 3 * nwaves;
+  // Exact ring waits for two to four tokens when each wave streams >= 12 records (two to four
+  // tokens, 18944 x 3584, 14 records: 11.3 / 13.8 / 13.8 us against 12.0 / 14.4 / 14.4; 25600 x
+  // 5120, 20 records: 15.9 / 18.1 / 18.7 against 16.9 / 19.0 / 19.5). With shorter parts the
+  // repeated loads cost more than the exact waits save (3584 x 18944, 10 records: 14.6 / 19.0 /
+  // 19.1 against 14.2 / 18.2 / 18.4), and one token is faster with the conditional refill at
+  // every shape (gate/up 10.2 against 11.5 us, 152064 x 3584 47 against 54 us).
+  const bool exact = MP > 1 && ceil_div(nblk, p.KW) >= 12;
   if (p.lds_x) {
     if (swiglu) {
       if (spread) FHIP_I8_LAUNCH(true, true, kXSpread, 2);
@@ -708,6 +725,7 @@ int launch_i8(const GemvGroup &g, const float *X, int K, int M, bool swiglu, voi
     else FHIP_I8_LAUNCH(false, false, kXLate, 2);
   }
 #undef FHIP_I8_LAUNCH
+#undef FHIP_I8_LAUNCH_EX
   FHIP_CHECK_LAUNCH("q4k_gemv_i8_kernel");
   return FHIP_OK;
 }
