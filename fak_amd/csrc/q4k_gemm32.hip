@@ -417,29 +417,28 @@ constexpr int wait_vm(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }  /
 
 // Q4_K: the staged form. Same 128-token x 128-row workgroup tile, grid and K order as
 // quant_gemm32_kernel (bit-identical results), but
-//   * each wave owns all 128 tokens x 128 / NW rows (4 x 4/NW MFMA tiles), so every dequantized
+//   * each of the four waves owns all 128 tokens x 32 rows (4 MFMA tiles), so every dequantized
 //     weight operand feeds four MFMAs instead of two and each weight is dequantized once per
 //     workgroup (the four-wave 2x2 form dequantizes every row twice);
 //   * activations go global -> LDS directly (global_load_lds_dwordx4, no staging registers) in
 //     8 KB stages of two K16 slices {h, 2 + h} of a 64-K chunk, four stage buffers, each stage
 //     loaded three stages ahead; every load is issued unconditionally (indices clamped at the
 //     end of K) so each wait is a compile-time count that leaves the later stages in flight;
-//   * the next super-block's records are loaded into registers at the first stage and written to
-//     LDS at the last one, so they get four stages to arrive.
-// NW = 4 (32 rows per wave, 166 VGPRs, 52 KB of LDS: three workgroups, 12 waves per CU) is the
-// default: with 592 workgroups at M=512 on 256 CUs its waves spread to at most three per SIMD
-// (NW = 2 puts two 64-row waves on some SIMDs and one on most). Measured at K=3584, N=18944
-// (us, NW=4 / NW=2 / four-wave 2x2): M=128 44.6 / - / 60.5, M=512 106.5 / 112.7 / 120,
-// M=2048 376 / 413 / 438; the down shape (K=18944, N=3584) at M=512 194 vs 274 (2x2).
-template <int NW>  // waves per workgroup: 2 (64 rows each) or 4 (32 rows each)
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2 ? 2 : 3, NW == 2 ? 2 : 3))) void q4k_gemm32s_kernel(
+//   * the weights go straight from the tiled records to the registers of the lanes that use
+//     them (a header and four nibble units per lane and super-block), with no LDS round trip and
+//     no second barrier per super-block (measured 4-5% faster than records staged through LDS
+//     at M = 128 / 512 / 2048: 41.5 / 97 / 367 us against 43.6 / 100-103 / 382-394).
+// 166 VGPRs and 33 KB of LDS: three workgroups (12 waves) per CU, so the 592 workgroups of
+// M=512 spread to at most three 32-row waves per SIMD. Two waves of 64 rows per workgroup
+// (256 VGPRs, two per SIMD) measured slower at every size (M=512 112.7 against 106.5 us, M=2048
+// 413 against 376, with the records still in LDS) and no longer fit their registers.
+constexpr int kGemmWaves = 4;
+__global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu(3, 3))) void q4k_gemm32s_kernel(
     const uint8_t *__restrict__ W, const uint4 *__restrict__ xa,
     const float *__restrict__ tscale, float *__restrict__ Y, int N,
     int M, int nblk, int ntiles, int MTG, int SK, float *__restrict__ part) {
-  constexpr int kRec = kQ4kRecord, kUnits = kQ4kRecord / 16;  // 144 units per record
-  constexpr int kWU = kBT * kUnits;                             // 1152 units per super-block
-  constexpr int kThreads = 64 * NW;
-  constexpr int kWPT = (kWU + kThreads - 1) / kThreads;         // 9 or 5 per thread
+  constexpr int NW = kGemmWaves;
+  constexpr int kUnits = kQ4kRecord / 16;                       // 144 units per record
   constexpr int kSU = 4 * 2 * 64;                               // 512 units (8 KB) per stage
   constexpr int NT = 4 / NW;                                    // 32-row MFMA tiles per wave
   constexpr int kDMA = 8 / NW;                                  // stage loads per wave
@@ -449,7 +448,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
   __shared__ u32x4 As1[kSU];
   __shared__ u32x4 As2[kSU];
   __shared__ u32x4 As3[kSU];
-  __shared__ u32x4 Ws[kWPT * kThreads];  // past kWU: padding (a repeat of unit 0)
   __shared__ __align__(16) float ts_lds[kBM];  // the token scales of this token tile
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -463,13 +461,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
   const Magic K = magic_consts();
   const u32x4 *xg = reinterpret_cast<const u32x4 *>(xa) + (size_t)(4 * mg) * nq * 64;
   const int tile0 = kBT * ng;
-  const u32x4 *Wv = reinterpret_cast<const u32x4 *>(W);
-  auto woff = [&](int k) {  // unit tid + kThreads k of the workgroup's 8 records (tile clamped)
-    const int u = tid + kThreads * k < kWU ? tid + kThreads * k : 0;
-    const int rec = u / kUnits, off = u - rec * kUnits;
-    const int T = min(tile0 + rec, ntiles - 1);
-    return (uint32_t)T * nblk * kUnits + off;
-  };
   // Stage s = 8 b + 2 c + h: slices 16 (4 b + c) + h + 2 hi of token tile i at [(2 i + hi) * 64],
   // one 1 KB wave load each; wave w loads units kDMA w .. kDMA w + kDMA - 1 (unit 2 i + hi).
   auto load_stage = [&](int s, u32x4 *dst) {
@@ -484,6 +475,35 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
   };
   auto buf = [&](int k) -> u32x4 * { return k == 0 ? As0 : k == 1 ? As1 : k == 2 ? As2 : As3; };
 
+  // The weights go straight to registers: lane (kap, rho) needs, per super-block and 32-row tile
+  // t, the 16 header bytes of row rho % 16 of 16-row tile tl(t) and four 16-byte units of nibble
+  // bytes (lane group 2 h + kap of chunks 2 c2, 2 c2 + 1). Rows past N read the last tile.
+  auto tl = [&](int t) { return (8 / NW) * wave + 2 * t + (rho >> 4); };
+  const int r16 = rho & 15;
+  const u32x4 *Wv = reinterpret_cast<const u32x4 *>(W);
+  auto rec = [&](int t, int b) {
+    return Wv + ((size_t)min(tile0 + tl(t), ntiles - 1) * nblk + b) * kUnits;
+  };
+  auto nib = [&](int c2, int h) { return kQ4kHdr / 16 + 64 * c2 + 16 * (2 * h + kap) + r16; };
+  u32x4 hdr[NT], u0[NT][2], u1[NT][2];
+  auto load_hu0 = [&](int b) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const u32x4 *r = rec(t, b);
+      hdr[t] = r[r16];
+      u0[t][0] = r[nib(0, 0)];
+      u0[t][1] = r[nib(0, 1)];
+    }
+  };
+  auto load_u1 = [&](int b) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const u32x4 *r = rec(t, b);
+      u1[t][0] = r[nib(1, 0)];
+      u1[t][1] = r[nib(1, 1)];
+    }
+  };
+
   f32x16 acc[4][NT];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -493,47 +513,58 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   const int nstage = (kb1 - kb0) * 8;
-  u32x4 wreg[kWPT];
-#pragma unroll
-  for (int k = 0; k < kWPT; ++k) wreg[k] = Wv[woff(k) + (uint32_t)kb0 * kUnits];
+  // Issue order as in the loop below at the start of a super-block: header and chunk 0-1
+  // units, then stages 0-2.
+  load_hu0(kb0);
   load_stage(0, As0);
   load_stage(1, As1);
   load_stage(2, As2);
-  for (int k = tid; k < kBM; k += kThreads) ts_lds[k] = tscale[kBM * mg + k];  // MTG * kBM entries
-#pragma unroll
-  for (int k = 0; k < kWPT; ++k) Ws[tid + kThreads * k] = wreg[k];
-  FHIP_LDS_BARRIER(wait_vm(0));
+  for (int k = tid; k < kBM; k += 64 * NW) ts_lds[k] = tscale[kBM * mg + k];  // MTG * kBM entries
+  FHIP_LDS_BARRIER(wait_vm(2 * kDMA));
 
-  // This lane's 16-row tiles: tile t of the wave is local tile (8 / NW) wave + 2 t + rho / 16.
-  auto tl = [&](int t) { return (8 / NW) * wave + 2 * t + (rho >> 4); };
-  const int r16 = rho & 15;
-  const unsigned char *wbase = reinterpret_cast<const unsigned char *>(Ws);
+  // A record register enters the arithmetic through an empty asm at the stage that first uses
+  // it: the compiler would otherwise hoist the dequantization next to the load and wait for it
+  // there (vmcnt(0)), with the registers of both held at once.
+  auto pin = [](u32x4 &v) { asm volatile("" : "+v"(v)); };
+  // The operand reads index the stage by an offset the compiler cannot see through. An LDS DMA's
+  // memory operand names only the first dword of its 1 KB wave block, so with a visible lane
+  // offset alias analysis proves some reads disjoint from every tracked DMA and the compiler
+  // falls back to waiting for all of them (vmcnt(0)); as a possible alias of its own buffer's
+  // DMA the read waits only for that buffer's loads, which the stage barrier already covers.
+  int alane = lane;
+  asm volatile("" : "+v"(alane));
   for (int b = kb0; b < kb1; ++b) {
     RowScales rs[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-      rs[t] = row_scales(__builtin_bit_cast(uint4, *reinterpret_cast<const u32x4 *>(wbase + tl(t) * kRec + 16 * r16)), K);
+    for (int t = 0; t < NT; ++t) {
+      pin(hdr[t]);
+      rs[t] = row_scales(__builtin_bit_cast(uint4, hdr[t]), K);
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
+      if (c == 0 || c == 2)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) pin(c == 0 ? u0[t][h] : u1[t][h]);
       uint2 xb[NT][2];  // nibble bytes of lane group g = 2 h + kap of chunk c, every row tile
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int T = tl(t);
-          xb[t][h] = *reinterpret_cast<const uint2 *>(wbase + T * kRec + kQ4kHdr + 1024 * (c >> 1) +
-                                                      16 * (16 * (2 * h + kap) + r16) + 8 * (c & 1));
+          const u32x4 v = c < 2 ? u0[t][h] : u1[t][h];
+          xb[t][h] = (c & 1) ? make_uint2(v[2], v[3]) : make_uint2(v[0], v[1]);
         }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int ls = 2 * c + h;  // stage within the super-block (its buffer is ls & 3)
         const int s = 8 * (b - kb0) + ls;
         load_stage(min(s + 3, nstage - 1), buf((ls + 3) & 3));
-        if (ls == 0) {
-          const uint32_t bn = (uint32_t)min(b + 1, kb1 - 1);
-#pragma unroll
-          for (int k = 0; k < kWPT; ++k) wreg[k] = Wv[woff(k) + bn * kUnits];
-        }
+        // Each record register is reloaded once its last use has been read out: chunk 2-3
+        // units of this super-block at stage 0 (used from stage 4), header and chunk 0-1 units
+        // of the next one at stage 4 (used from its stage 0).
+        if (ls == 0) load_u1(b);
+        if (ls == 4) load_hu0(min(b + 1, kb1 - 1));
         const u32x4 *Acur = buf(ls & 3);
         f16x8 bl[NT], bh[NT];
 #pragma unroll
@@ -542,24 +573,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2
         for (int hi = 0; hi < 2; ++hi) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const f16x8 a = __builtin_bit_cast(f16x8, Acur[(2 * i + hi) * 64 + lane]);
+            const f16x8 a = __builtin_bit_cast(f16x8, Acur[(2 * i + hi) * 64 + alane]);
 #pragma unroll
             for (int t = 0; t < NT; ++t)
               acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, hi ? bh[t] : bl[t], acc[i][t], 0, 0, 0);
           }
         }
-        if (ls == 7) {
-          FHIP_LDS_BARRIER(wait_vm(63));  // every wave is done reading this super-block's records
-#pragma unroll
-          for (int k = 0; k < kWPT; ++k) Ws[tid + kThreads * k] = wreg[k];
-        }
-        // Stage s + 1 has landed once at most this many of this wave's later loads are pending:
-        // stages s + 2 and s + 3 (kDMA loads each) and, during stages 0-2, the kWPT record
-        // loads that went out after stage s + 1's.
-        if (ls <= 2)
-          FHIP_LDS_BARRIER(wait_vm(2 * kDMA + kWPT));
-        else
-          FHIP_LDS_BARRIER(wait_vm(2 * kDMA));
+        // Stage s + 1 has landed (for every wave, after the barrier) once at most stages s + 2
+        // and s + 3 (kDMA loads each) are pending. The record loads of this stage complete by
+        // then too: with plain loads still pending beside the LDS DMA the compiler no longer
+        // trusts the counter's order and waits for all loads (vmcnt(0)) before the next stage's
+        // operand reads; letting them stay in flight that way measured no faster.
+        FHIP_LDS_BARRIER(wait_vm(2 * kDMA));
       }
     }
   }
@@ -623,15 +648,15 @@ GemmPlan plan_gemm32(int fmt, int N, int K, int M) {
   const int nblk = K / 256;
   p.MTG = ceil_div(M, kBM);
   p.grid = p.MTG * ceil_div(q4k_tiles(N), kBT);
-  // FAK_HIP_GEMM32_FORM: 1 = the four-wave 2x2 kernel, 2 = the staged kernel with two waves of
-  // 64 rows (comparisons; all forms agree bit for bit without a K split). Default: the staged
-  // kernel with four waves of 32 rows, measured faster than the others from 64 to 2048 tokens.
+  // FAK_HIP_GEMM32_FORM=1: the four-wave 2x2 kernel (a comparison; it agrees bit for bit with
+  // the default without a K split). Default: the staged kernel, measured faster from 64 to 2048
+  // tokens.
   p.form = fmt == 0 ? tuning().gemm32_form : 1;
   // K split of the default form when the grid does not fill the GPU (e.g. the 3584-row down
   // projection, or 128 tokens): about two workgroups per CU, ranges of at least 4 super-blocks;
   // the partial results are added in range order. FAK_HIP_GEMM32_SK overrides.
   p.SK = 1;
-  if (p.form != 1 && p.form != 2) {
+  if (p.form != 1) {
     const int cus = cu_count() > 0 ? cu_count() : 256;
     p.SK = tuning().gemm32_sk;
     if (p.SK <= 0) p.SK = p.grid < cus ? min(ceil_div(2 * cus, p.grid), nblk / 4) : 1;
@@ -663,15 +688,9 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
     FHIP_CHECK_LAUNCH("quant_gemm32_kernel");
     return FHIP_OK;
   }
-  if (p.form == 2) {
-    q4k_gemm32s_kernel<2><<<grid, 128, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles, MTG, 1,
-                                                       nullptr);
-    FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
-    return FHIP_OK;
-  }
   if (p.form != 1) {
-    q4k_gemm32s_kernel<4><<<grid * SK, 256, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles, MTG,
-                                                            SK, part);
+    q4k_gemm32s_kernel<<<grid * SK, 64 * kGemmWaves, 0, stream()>>>(W, xa, ts, Y, N, M, nblk,
+                                                                     ntiles, MTG, SK, part);
     FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
     if (SK > 1) {
       const long long tot = (long long)M * N;

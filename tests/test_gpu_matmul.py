@@ -200,32 +200,29 @@ def test_q4k_gemm_prefill_7b(hip, oracle_mod, P):
 @pytest.mark.parametrize("out,in_,P", [(300, 768, 600), (1000, 2048, 520), (64, 256, 1000),
                                        (18944, 3584, 512)])
 def test_q4k_gemm_forms_bit_identical(hip, oracle_mod, monkeypatch, out, in_, P):
-    """The staged GEMM (four waves of 32 rows: the default; or two waves of 64 rows) and the
-    four-wave 2x2 GEMM share the tile, the K order and each accumulator's MFMA sequence: their
-    outputs agree bit for bit, on
-    whole and ragged row / token tiles, and the staged result meets the GEMM bound against the
-    oracle (sampled rows at the 7B shape)."""
+    """The staged GEMM (the default: four waves of 32 rows, weights loaded straight to the
+    registers of the lanes that use them) and the four-wave 2x2 GEMM (records staged through LDS)
+    share the tile, the K order and each accumulator's MFMA sequence: their outputs agree bit
+    for bit, on whole and ragged row / token tiles, and the staged result meets the GEMM bound
+    against the oracle (sampled rows at the 7B shape)."""
     print(f"[case] gemm forms out={out} in={in_} P={P}", flush=True)
     raw = synth.q4k_weights(out, in_, seed=out + 3 * P)
     X = synth.activations(P, in_, seed=P + 5)
     with knobs(monkeypatch, FAK_HIP_GEMM32_FORM=1):
         Y1 = q4k_matmul(raw, out, in_, X, P)
-    with knobs(monkeypatch, FAK_HIP_GEMM32_FORM=2):
-        Y2 = q4k_matmul(raw, out, in_, X, P)
     # the default form with no K split: the same summation order
-    with knobs(monkeypatch, FAK_HIP_GEMM32_FORM=3, FAK_HIP_GEMM32_SK=1):
+    with knobs(monkeypatch, FAK_HIP_GEMM32_SK=1):
         Y3 = q4k_matmul(raw, out, in_, X, P)
-    assert np.array_equal(Y1.view(np.uint32), Y2.view(np.uint32))
     assert np.array_equal(Y1.view(np.uint32), Y3.view(np.uint32))
     if out > 4096:
         rb = (in_ // 256) * 144
         sel = np.concatenate([np.arange(0, 128), np.arange(out - 128, out)])
         sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
         ref = oracle_mod.q4k_gemm(sub, len(sel), in_, X, P, workers=16)
-        got = Y2[:, sel]
+        got = Y3[:, sel]
     else:
         ref = oracle_mod.q4k_gemm(raw, out, in_, X, P, workers=16)
-        got = Y2
+        got = Y3
     assert rel_err(got, ref) <= GEMM_TOL
 
 
