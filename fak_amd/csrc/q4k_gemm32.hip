@@ -121,6 +121,7 @@ __device__ __forceinline__ void dequant6(uint2 qa, uint2 qb, uint2 qh, int k, _F
 
 constexpr int kBM = 128;               // tokens per workgroup
 constexpr int kBT = 8;                 // 16-row tiles per workgroup (128 rows)
+constexpr int kTileElems = kBM * 128;  // outputs of one workgroup tile
 constexpr int kAU = 4 * 4 * 64;        // uint4 units of one activation stage (4 tiles x 4 K16)
 
 // Per weight format: record bytes, uint4 units of one super-block's records for the workgroup's
@@ -140,9 +141,13 @@ struct GemmFmt {
 // finite f32 row converts to f16 without overflow and keeps 11-bit relative precision down to
 // 2^-28 of its maximum; the GEMM multiplies the token's outputs by tscale[t] = 2^k (exact), NaN
 // for a row holding a NaN or an infinity (its operands are zeros), 1 for an all-zero row.
-// One workgroup per (padded) token: a max-reduce over the row, then the conversion (the second
-// read of the row hits L2).
+// One workgroup per (padded) token: a max-reduce over the row, then the conversion. UPT > 0: each
+// thread loads its UPT 8-value units of the row at once (unconditionally, indices clamped to the
+// row; a repeated unit changes neither the maximum nor the NaN flag) and converts them from its
+// registers, so the row is read once with every load in flight together (rows of K <= 2048 UPT).
+// UPT = 0: a loop over the row, read twice (the second pass hits L2), for longer rows.
 constexpr int kXprepThreads = 256;
+template <int UPT>
 __global__ __launch_bounds__(kXprepThreads) void gemm32_xprep_kernel(
     const float *__restrict__ X, int M, int K, uint4 *__restrict__ xa, float *__restrict__ tscale) {
   __shared__ float wmax[kXprepThreads / 64];
@@ -153,12 +158,27 @@ __global__ __launch_bounds__(kXprepThreads) void gemm32_xprep_kernel(
   // fmaxf drops NaN: a NaN anywhere must still mark the row, so it is tracked separately.
   float amax = 0.f;
   bool bad = false;
-  if (valid)
-    for (int i = tid; i < K / 4; i += kXprepThreads) {
-      const float4 v = row[i];
-      amax = fmaxf(fmaxf(amax, fabsf(v.x)), fmaxf(fmaxf(fabsf(v.y), fabsf(v.z)), fabsf(v.w)));
-      bad |= (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
+  auto see = [&](const float4 v) {
+    amax = fmaxf(fmaxf(amax, fabsf(v.x)), fmaxf(fmaxf(fabsf(v.y), fabsf(v.z)), fabsf(v.w)));
+    bad |= (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
+  };
+  float4 reg[UPT > 0 ? UPT : 1][2];
+  if (UPT > 0) {
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) {
+      const int u = min(tid + j * kXprepThreads, nu - 1);
+      reg[j][0] = row[2 * u];
+      reg[j][1] = row[2 * u + 1];
     }
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) {
+      see(reg[j][0]);
+      see(reg[j][1]);
+    }
+  } else {
+    for (int i = tid; i < K / 4; i += kXprepThreads) see(row[i]);
+  }
+  if (!valid) amax = 0.f, bad = false;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
   const bool wbad = __any(bad);
@@ -177,11 +197,10 @@ __global__ __launch_bounds__(kXprepThreads) void gemm32_xprep_kernel(
   const int k = E - 15;  // m / 2^k in [2^14, 2^15)
   if (tid == 0) tscale[t] = !finite ? __builtin_nanf("") : m > 0.f ? ldexpf(1.f, k) : 1.f;
   const int tt = t >> 5, lt = t & 31;
-  for (int u = tid; u < nu; u += kXprepThreads) {
+  auto put = [&](int u, const float4 v0, const float4 v1) {
     const int q = u >> 1, half = u & 1;
     f16x8 h;
     if (valid && finite) {
-      const float4 v0 = row[2 * u], v1 = row[2 * u + 1];
       const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
       for (int j = 0; j < 8; ++j) h[j] = (_Float16)ldexpf(v[perm8(j)], -k);
@@ -190,7 +209,34 @@ __global__ __launch_bounds__(kXprepThreads) void gemm32_xprep_kernel(
       for (int j = 0; j < 8; ++j) h[j] = (_Float16)0.f;
     }
     xa[((size_t)tt * nq + q) * 64 + 32 * half + lt] = __builtin_bit_cast(uint4, h);
+  };
+  if (UPT > 0) {
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) {
+      const int u = tid + j * kXprepThreads;
+      if (u < nu) put(u, reg[j][0], reg[j][1]);
+    }
+  } else {
+    for (int u = tid; u < nu; u += kXprepThreads) put(u, row[2 * u], row[2 * u + 1]);
   }
+}
+
+// Launches the activation prep with the smallest register-resident unit count that covers K.
+void launch_xprep(const float *X, int M, int K, int MTG, uint4 *xa, float *ts) {
+  const int upt = ceil_div(K / 8, kXprepThreads);
+  const unsigned grid = MTG * kBM;
+  if (upt <= 2)
+    gemm32_xprep_kernel<2><<<grid, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
+  else if (upt <= 4)
+    gemm32_xprep_kernel<4><<<grid, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
+  else if (upt <= 8)
+    gemm32_xprep_kernel<8><<<grid, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
+  else if (upt <= 12)
+    gemm32_xprep_kernel<12><<<grid, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
+  else if (upt <= 16)
+    gemm32_xprep_kernel<16><<<grid, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
+  else
+    gemm32_xprep_kernel<0><<<grid, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
 }
 
 // FMT: 0 Q4_K, 1 Q6_K. NWB: LDS buffers for the weight records (2: the next super-block loads
@@ -436,7 +482,7 @@ constexpr int kGemmWaves = 4;
 __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu(3, 3))) void q4k_gemm32s_kernel(
     const uint8_t *__restrict__ W, const uint4 *__restrict__ xa,
     const float *__restrict__ tscale, float *__restrict__ Y, int N,
-    int M, int nblk, int ntiles, int MTG, int SK, float *__restrict__ part) {
+    int M, int nblk, int ntiles, int MTG, int F, int S, int R, float *__restrict__ part) {
   constexpr int NW = kGemmWaves;
   constexpr int kUnits = kQ4kRecord / 16;                       // 144 units per record
   constexpr int kSU = 4 * 2 * 64;                               // 512 units (8 KB) per stage
@@ -452,11 +498,15 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kap = lane >> 5, rho = lane & 31;
-  // Workgroup = (tile, K range sp): SK > 1 splits K for grids too small to fill the GPU; each
-  // range writes its partial sums and a second kernel adds them in range order.
-  const int task = blockIdx.x / SK, sp = blockIdx.x - task * SK;
+  // Workgroup -> (tile task, K range sp of ns): the first F workgroups run whole tiles, the
+  // next R * S the last R tiles in S K ranges each. Range 0 writes Y, the others their partial
+  // sums, which gemm32_reduce_kernel adds to Y in range order.
+  const int w = blockIdx.x;
+  const bool split = w >= F;
+  const int pw = split ? w - F : 0;
+  const int task = split ? F + pw / S : w, sp = split ? pw % S : 0, ns = split ? S : 1;
   const int mg = task % MTG, ng = task / MTG;
-  const int kb0 = sp * nblk / SK, kb1 = (sp + 1) * nblk / SK;  // >= 1 super-block: SK <= nblk
+  const int kb0 = sp * nblk / ns, kb1 = (sp + 1) * nblk / ns;  // >= 1 super-block: S <= nblk
   const int nq = nblk * 16;
   const Magic K = magic_consts();
   const u32x4 *xg = reinterpret_cast<const u32x4 *>(xa) + (size_t)(4 * mg) * nq * 64;
@@ -611,10 +661,11 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
         const int tok = t0 + 8 * (v >> 2) + (v & 3);
         if (tok >= M) continue;
         const float val = acc[i][t][v] * sc[v];
-        if (SK == 1)
+        if (sp == 0)
           Y[(size_t)tok * N + o] = val;
         else
-          part[((size_t)sp * M + tok) * N + o] = val;
+          part[((size_t)(sp - 1) * R + (task - F)) * kTileElems + (tok - kBM * mg) * 128 +
+               (o - 128 * ng)] = val;
       }
     }
   }
@@ -622,14 +673,32 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
 #undef FHIP_LDS_BARRIER
 
 
-// Y = the SK partial results of a K-split GEMM added in range order (deterministic).
-__global__ void gemm32_reduce_kernel(const float *__restrict__ part, float *__restrict__ Y, int SK,
-                                     long long total) {
-  const long long id = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= total) return;
-  float v = part[id];
-  for (int s = 1; s < SK; ++s) v += part[(size_t)s * total + id];
-  Y[id] = v;
+// Y += the partial sums of K ranges 1 .. S-1 of the R split tiles (tasks F .. F+R-1), added in
+// range order after range 0, which the GEMM wrote to Y (deterministic). part holds 128 x 128
+// f32 per (range, tile), token-major. Each thread adds four outputs of one token row.
+__global__ __launch_bounds__(256) void gemm32_reduce_kernel(const float *__restrict__ part,
+                                                            float *__restrict__ Y, int N, int M,
+                                                            int MTG, int F, int S, int R) {
+  constexpr int kQuads = kTileElems / 4;
+  const long long id = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (id >= (long long)R * kQuads) return;
+  const int r = (int)(id / kQuads), e4 = (int)(id - (long long)r * kQuads);
+  const int task = F + r, mg = task % MTG, ng = task / MTG;
+  const int tok = kBM * mg + (e4 >> 5), o0 = 128 * ng + 4 * (e4 & 31);
+  if (tok >= M || o0 >= N) return;
+  const float4 *pp = reinterpret_cast<const float4 *>(part) + (size_t)r * kQuads + e4;
+  float *y = Y + (size_t)tok * N + o0;
+  const int nv = min(4, N - o0);
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = j < nv ? y[j] : 0.f;
+  for (int s = 1; s < S; ++s) {
+    const float4 q = pp[(size_t)(s - 1) * R * kQuads];
+    v[0] += q.x; v[1] += q.y; v[2] += q.z; v[3] += q.w;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (j < nv) y[j] = v[j];
 }
 
 }  // namespace
@@ -639,7 +708,7 @@ namespace {
 // Launch plan of one GEMM call: form, K split and the scratch it needs (activation operands,
 // token scales, then the K-range partial results).
 struct GemmPlan {
-  int MTG, grid, form, SK;
+  int MTG, tasks, form, F, S, R;  // tile tasks; F whole, then R split into S K ranges each
   size_t xab, tsb, pb;
 };
 
@@ -647,25 +716,47 @@ GemmPlan plan_gemm32(int fmt, int N, int K, int M) {
   GemmPlan p{};
   const int nblk = K / 256;
   p.MTG = ceil_div(M, kBM);
-  p.grid = p.MTG * ceil_div(q4k_tiles(N), kBT);
+  p.tasks = p.MTG * ceil_div(q4k_tiles(N), kBT);
   // FAK_HIP_GEMM32_FORM=1: the four-wave 2x2 kernel (a comparison; it agrees bit for bit with
   // the default without a K split). Default: the staged kernel, measured faster from 64 to 2048
   // tokens.
   p.form = fmt == 0 ? tuning().gemm32_form : 1;
-  // K split of the default form when the grid does not fill the GPU (e.g. the 3584-row down
-  // projection, or 128 tokens): about two workgroups per CU, ranges of at least 4 super-blocks;
-  // the partial results are added in range order. FAK_HIP_GEMM32_SK overrides.
-  p.SK = 1;
+  p.F = p.tasks;
+  p.S = 1;
+  p.R = 0;
   if (p.form != 1) {
+    // K splits of the staged kernel (partial sums added in range order):
+    //  * a grid smaller than the GPU (the 3584-row down projection, or 128 tokens) splits every
+    //    tile into as many ranges as keep the grid within two workgroups per CU (at least 4
+    //    super-blocks each): a third workgroup on some CUs sets the time (down projection at
+    //    M=512: 4 ranges 116 us, 5 ranges 128 us; 27B gate/up at M=128: 2 ranges 62 us, 3: 66);
+    //  * a larger grid runs whole tiles in rounds of one per CU and splits only the tiles of
+    //    the last, partial round, so that every CU gets the same whole tiles plus at most one
+    //    range (M=512 on the gate/up shape: 512 whole tiles and 80 tiles in 3 ranges, where 80
+    //    CUs ran a third whole tile; ranges of at least 2 super-blocks);
+    //  * FAK_HIP_GEMM32_SK=n splits every tile in n (1: no split).
     const int cus = cu_count() > 0 ? cu_count() : 256;
-    p.SK = tuning().gemm32_sk;
-    if (p.SK <= 0) p.SK = p.grid < cus ? min(ceil_div(2 * cus, p.grid), nblk / 4) : 1;
-    if (p.SK < 1) p.SK = 1;
-    if (p.SK > nblk) p.SK = nblk;
+    const int sk = tuning().gemm32_sk;
+    int S = 1, R = 0;
+    if (sk > 0) {
+      S = min(sk, nblk);
+      R = p.tasks;
+    } else if (p.tasks < cus) {
+      S = min(2 * cus / p.tasks, nblk / 4);
+      R = p.tasks;
+    } else if (p.tasks % cus) {
+      R = p.tasks % cus;
+      S = min(cus / R, nblk / 2);
+    }
+    if (S > 1) {
+      p.S = S;
+      p.R = R;
+      p.F = p.tasks - R;
+    }
   }
   p.xab = ((size_t)p.MTG * kBM * K * 2 + 255) & ~(size_t)255;
   p.tsb = ((size_t)p.MTG * kBM * 4 + 255) & ~(size_t)255;
-  p.pb = p.SK > 1 ? (size_t)p.SK * M * N * 4 : 0;
+  p.pb = p.R ? (size_t)(p.S - 1) * p.R * kTileElems * 4 : 0;
   return p;
 }
 
@@ -673,14 +764,14 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
   const int nblk = K / 256;
   const int ntiles = q4k_tiles(N);
   const GemmPlan p = plan_gemm32(fmt, N, K, M);
-  const int MTG = p.MTG, grid = p.grid, SK = p.SK;
+  const int MTG = p.MTG, grid = p.tasks;
   unsigned char *ws = (unsigned char *)workspace(p.xab + p.tsb + p.pb);
   if (!ws) return FHIP_ENOMEM;
   if (int rc = check_disjoint("gemm32", X, (size_t)M * K * 4, ws, p.xab + p.tsb + p.pb)) return rc;
   uint4 *xa = (uint4 *)ws;
   float *ts = (float *)(ws + p.xab);
-  float *part = SK > 1 ? (float *)(ws + p.xab + p.tsb) : nullptr;
-  gemm32_xprep_kernel<<<MTG * kBM, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
+  float *part = p.R ? (float *)(ws + p.xab + p.tsb) : nullptr;
+  launch_xprep(X, M, K, MTG, xa, ts);
   FHIP_CHECK_LAUNCH("gemm32_xprep_kernel");
   const uint8_t *W = (const uint8_t *)Wv;
   if (fmt == 1) {  // 60 KB of LDS with one weight buffer: two workgroups per CU
@@ -689,12 +780,13 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
     return FHIP_OK;
   }
   if (p.form != 1) {
-    q4k_gemm32s_kernel<<<grid * SK, 64 * kGemmWaves, 0, stream()>>>(W, xa, ts, Y, N, M, nblk,
-                                                                     ntiles, MTG, SK, part);
+    q4k_gemm32s_kernel<<<p.F + p.R * p.S, 64 * kGemmWaves, 0, stream()>>>(
+        W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
     FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
-    if (SK > 1) {
-      const long long tot = (long long)M * N;
-      gemm32_reduce_kernel<<<(unsigned)((tot + 255) / 256), 256, 0, stream()>>>(part, Y, SK, tot);
+    if (p.R) {
+      const long long quads = (long long)p.R * (kTileElems / 4);
+      gemm32_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, stream()>>>(
+          part, Y, N, M, MTG, p.F, p.S, p.R);
       FHIP_CHECK_LAUNCH("gemm32_reduce_kernel");
     }
     return FHIP_OK;

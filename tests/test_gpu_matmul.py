@@ -249,6 +249,29 @@ def test_q4k_gemm_k_split(hip, oracle_mod, out, in_, P):
     assert rel_err(got, ref) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("out,in_,P", [(18900, 3584, 500), (18900, 1024, 500), (18944, 3584, 2048)])
+def test_q4k_gemm_tail_split(hip, oracle_mod, monkeypatch, out, in_, P):
+    """Grids of more tiles than CUs run whole tiles in rounds of one per CU and split only the
+    last, partial round's tiles into K ranges (range 0 in Y, the rest added in range order). On
+    ragged row and token tiles: the first row block (whole tiles) is bit-identical to the
+    unsplit kernel, the last rows (split tiles) meet the GEMM bound against the oracle, and the
+    result is the same bits call after call."""
+    print(f"[case] gemm tail split out={out} in={in_} P={P}", flush=True)
+    raw = synth.q4k_weights(out, in_, seed=out + 13 * P)
+    X = synth.activations(P, in_, seed=P + 17)
+    Y = q4k_matmul(raw, out, in_, X, P)
+    assert np.array_equal(Y.view(np.uint32), q4k_matmul(raw, out, in_, X, P).view(np.uint32))
+    with knobs(monkeypatch, FAK_HIP_GEMM32_SK=1):
+        Y1 = q4k_matmul(raw, out, in_, X, P)
+    assert np.array_equal(Y[:, :128].view(np.uint32), Y1[:, :128].view(np.uint32))
+    rb = (in_ // 256) * 144
+    sel = np.concatenate([np.arange(0, 16), np.arange(out - 112, out)])
+    sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
+    ref = oracle_mod.q4k_gemm(sub, len(sel), in_, X, P, workers=16)
+    assert rel_err(Y[:, sel], ref) <= GEMM_TOL
+    assert rel_err(Y[:, out - 112:], Y1[:, out - 112:]) <= GEMM_TOL
+
+
 def test_q4k_gemm_equals_gemv_per_token_within_tolerance(hip, oracle_mod):
     """The reference pins GEMM(o,t) == GEMV(X_t)(o) bitwise on the CPU; on the device the two
     kernels use different precisions, so each is held to its own bound against the same oracle

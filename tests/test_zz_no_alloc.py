@@ -47,7 +47,7 @@ def test_noalloc_matches_allocating_entry(hip, oracle_mod, first, second):
 
 def test_noalloc_refuses_oversized_scratch(hip):
     lib = fakhip.load()
-    out, in_, P = 3584, 18944, 1024  # prefill operands + partials > 64 MiB
+    out, in_, P = 3584, 18944, 2048  # f16 prefill operands alone: 77.6 MB > 64 MiB
     raw = synth.q4k_weights(out, in_, 3)  # kept alive across the upload's host read
     w = fakhip.alloc_call("fhip_q4k_upload", raw.ctypes.data, out, in_)
     try:
