@@ -89,6 +89,23 @@ __device__ __forceinline__ uint16_t ld_stream16(const void *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
 }
 
+// Ordered sum of K-range partial results: v (range 0) += p1[k * stride] for k = 0 .. count-1
+// (ranges 1 .. count), in that order. The loads go out eight at a time (indices clamped, so
+// every load is issued; a repeated one is not added): a loop of run-time length would wait for
+// each load before issuing the next.
+template <typename T>
+__device__ __forceinline__ T add_ranges(T v, const T *__restrict__ p1, size_t stride, int count) {
+  for (int k = 0; k < count; k += 8) {
+    T q[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = p1[(size_t)min(k + j, count - 1) * stride];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (k + j < count) v = v + q[j];
+  }
+  return v;
+}
+
 // Two-digit int8 activations: the digits of four values x at scale 2^sh (|x| 2^sh <= 32512): y = x 2^sh + (1.5 2^23 + 128)
 // lies in [2^23, 2^24), where floats are the integers, so the add rounds x 2^sh half to even
 // exactly as rint and the low 23 bits of y hold 2^22 + T + 128. Byte 1 of y is then

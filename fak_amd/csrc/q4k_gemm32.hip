@@ -686,19 +686,21 @@ __global__ __launch_bounds__(256) void gemm32_reduce_kernel(const float *__restr
   const int task = F + r, mg = task % MTG, ng = task / MTG;
   const int tok = kBM * mg + (e4 >> 5), o0 = 128 * ng + 4 * (e4 & 31);
   if (tok >= M || o0 >= N) return;
+  // Range s (1 .. S-1) of this tile's quad: part + ((s - 1) R + r) kQuads + e4.
   const float4 *pp = reinterpret_cast<const float4 *>(part) + (size_t)r * kQuads + e4;
   float *y = Y + (size_t)tok * N + o0;
   const int nv = min(4, N - o0);
-  float v[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = j < nv ? y[j] : 0.f;
-  for (int s = 1; s < S; ++s) {
-    const float4 q = pp[(size_t)(s - 1) * R * kQuads];
-    v[0] += q.x; v[1] += q.y; v[2] += q.z; v[3] += q.w;
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (j < nv) y[j] = v[j];
+  float4 v0;
+  v0.x = y[0];
+  v0.y = nv > 1 ? y[1] : 0.f;
+  v0.z = nv > 2 ? y[2] : 0.f;
+  v0.w = nv > 3 ? y[3] : 0.f;
+  const size_t stride = (size_t)R * kQuads;
+  const float4 v = add_ranges(v0, pp, stride, S - 1);
+  y[0] = v.x;
+  if (nv > 1) y[1] = v.y;
+  if (nv > 2) y[2] = v.z;
+  if (nv > 3) y[3] = v.w;
 }
 
 }  // namespace

@@ -472,24 +472,14 @@ __global__ void gemv16_reduce1_kernel(const float *__restrict__ part, float *__r
                                       int SK, int total) {
   const int id = blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= total) return;
-  float v = part[id];
-  for (int s = 1; s < SK; ++s) v += part[(size_t)s * total + id];
-  Y[id] = v;
+  Y[id] = add_ranges(part[id], part + total + id, (size_t)total, SK - 1);
 }
 
 __global__ void gemv16_reduce_kernel(const float4 *__restrict__ part, float4 *__restrict__ Y,
                                      int SK, int total4) {
   const int id = blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= total4) return;
-  float4 v = part[id];
-  for (int s = 1; s < SK; ++s) {
-    const float4 p = part[(size_t)s * total4 + id];
-    v.x += p.x;
-    v.y += p.y;
-    v.z += p.z;
-    v.w += p.w;
-  }
-  Y[id] = v;
+  Y[id] = add_ranges(part[id], part + total4 + id, (size_t)total4, SK - 1);
 }
 
 }  // namespace
