@@ -592,6 +592,10 @@ void i8_shape(int ntiles, int nblk, int max_waves, size_t lds_fixed, size_t lds_
       TW = 4 / KW > 1 ? 4 / KW : 1;
     } else {
       while (TW > 1 && ceil_div(ntiles, TW) < cus / 2) TW /= 2;
+      // A grid of about 80% of the CUs beats wider workgroups on fewer CUs (one token, 7B
+      // gate/up, 1184 tiles: 6 tiles per workgroup 9.55 us, 5 9.6, 8 10.2; 27B gate/up, 1600
+      // tiles: 8 either way, 14.7 us; a grid beyond the CU count runs a second round, 20.9 us).
+      TW = min(TW, max(1, ceil_div(5 * ntiles, 4 * cus)));
       auto rounds = [&](int tw, int kw) {
         const size_t lds = lds_fixed + (size_t)tw * kw * lds_per_wave;
         const int by_lds = lds > 0 ? (int)(lds_max / lds) : 32;
