@@ -576,13 +576,6 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
   // it: the compiler would otherwise hoist the dequantization next to the load and wait for it
   // there (vmcnt(0)), with the registers of both held at once.
   auto pin = [](u32x4 &v) { asm volatile("" : "+v"(v)); };
-  // The operand reads index the stage by an offset the compiler cannot see through. An LDS DMA's
-  // memory operand names only the first dword of its 1 KB wave block, so with a visible lane
-  // offset alias analysis proves some reads disjoint from every tracked DMA and the compiler
-  // falls back to waiting for all of them (vmcnt(0)); as a possible alias of its own buffer's
-  // DMA the read waits only for that buffer's loads, which the stage barrier already covers.
-  int alane = lane;
-  asm volatile("" : "+v"(alane));
   for (int b = kb0; b < kb1; ++b) {
     RowScales rs[NT];
 #pragma unroll
@@ -623,7 +616,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
         for (int hi = 0; hi < 2; ++hi) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const f16x8 a = __builtin_bit_cast(f16x8, Acur[(2 * i + hi) * 64 + alane]);
+            const f16x8 a = __builtin_bit_cast(f16x8, Acur[(2 * i + hi) * 64 + lane]);
 #pragma unroll
             for (int t = 0; t < NT; ++t)
               acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, hi ? bh[t] : bl[t], acc[i][t], 0, 0, 0);
