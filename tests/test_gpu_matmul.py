@@ -61,6 +61,13 @@ def test_q4k_lm_head_7b(hip, oracle_mod):
     _check_q4k(oracle_mod, 152064, 3584, 1, seed=152064, tol=GEMV_TOL)
 
 
+@pytest.mark.parametrize("P", [2, 3, 4])
+def test_q4k_gemv_7b_gateup_2_to_4_tokens(hip, oracle_mod, P):
+    """Two to four tokens on the 7B gate/up shape: one-wave tiles streaming 14 records each, the
+    ring refilled unconditionally so every ring wait counts exactly; every output checked."""
+    _check_q4k(oracle_mod, 18944, 3584, P, seed=4096 + P, tol=GEMV_TOL)
+
+
 @pytest.mark.parametrize("out,in_,P", [(5120, 25600, 2), (3584, 18944, 3), (3584, 18944, 4)])
 def test_q4k_gemv_global_operands_natural(hip, oracle_mod, out, in_, P):
     """Shapes whose activation operands do not fit in LDS, so the GEMV takes its global-operand
@@ -80,6 +87,7 @@ def test_q4k_gemv_global_operands_forced(hip, oracle_mod, monkeypatch, out, in_,
         glob = q4k_matmul(raw, out, in_, X, P)
     ref = oracle_mod.q4k_gemm(raw, out, in_, X, P, workers=16)
     assert rel_err(glob, ref) <= GEMV_TOL
+    assert np.array_equal(glob.view(np.uint32), lds.view(np.uint32))
     assert np.array_equal(lds.view(np.uint32), glob.view(np.uint32))
 
 
