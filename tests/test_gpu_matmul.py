@@ -257,7 +257,8 @@ def test_q4k_gemm_k_split(hip, oracle_mod, out, in_, P):
     assert rel_err(got, ref) <= GEMM_TOL
 
 
-@pytest.mark.parametrize("out,in_,P", [(18900, 3584, 500), (18900, 1024, 500), (18944, 3584, 2048)])
+@pytest.mark.parametrize("out,in_,P", [(18900, 3584, 500), (18900, 1024, 500), (18944, 3584, 256),
+                                       (18944, 3584, 2048)])
 def test_q4k_gemm_tail_split(hip, oracle_mod, monkeypatch, out, in_, P):
     """Grids of more tiles than CUs run whole tiles in rounds of one per CU and split only the
     last, partial round's tiles into K ranges (range 0 in Y, the rest added in range order). On
