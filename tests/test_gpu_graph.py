@@ -13,7 +13,8 @@ pytestmark = pytest.mark.gpu
 
 
 def test_graph_replays_match_eager(hip):
-    print("[case] graph capture: q4k gemv/group/gemm, hal q8, gguf q8_0", flush=True)
+    print("[case] graph capture: q4k gemv/group/gemm (unsplit, K-split, tail split), hal q8, "
+          "gguf q8_0", flush=True)
     lib = fakhip.load()
     st = C.c_void_p()
     fakhip.call("fhip_stream_create", C.byref(st))
@@ -28,15 +29,24 @@ def test_graph_replays_match_eager(hip):
               for r in rg]
         r8 = synth.q8_0_weights(512, K, 15)
         w8 = fakhip.alloc_call("fhip_q8_0_upload", r8.ctypes.data, 512, K)
-        allocs += [w1, w8] + wg
+        # Prefill GEMMs that split K: 8 tiles in 4 K ranges (a grid smaller than the GPU), and
+        # 258 tiles of which the last partial round (2 tiles) is split; both end in the reduce.
+        K4, NT = 4 * K, 33024
+        rs = synth.q4k_weights(1024, K4, 16)
+        ws = fakhip.alloc_call("fhip_q4k_upload", rs.ctypes.data, 1024, K4)
+        rt = synth.q4k_weights(NT, K, 17)
+        wt = fakhip.alloc_call("fhip_q4k_upload", rt.ctypes.data, NT, K)
+        allocs += [w1, w8, ws, wt] + wg
         rng = np.random.default_rng(7)
         codes = Dev.from_host(rng.integers(-127, 128, 320 * K, dtype=np.int8))
         scales = Dev.from_host((np.abs(rng.standard_normal(320 * K // 32)) * 0.01).astype(np.float32))
         x1 = Dev(K * 4)
         x40 = Dev(40 * K * 4)
-        devs += [codes, scales, x1, x40]
+        x40b = Dev(40 * K4 * 4)
+        devs += [codes, scales, x1, x40, x40b]
         outs = {name: (Dev(n * 4), Dev(n * 4)) for name, n in
                 [("gemv", 1024), ("g0", 1024), ("g1", 256), ("g2", 256), ("gemm", 40 * 1024),
+                 ("gemm_split", 40 * 1024), ("gemm_tail", 40 * NT),
                  ("q8", 320), ("q8b", 4 * 320), ("gguf", 512)]}
         for a, b in outs.values():
             devs += [a, b]
@@ -52,6 +62,9 @@ def test_graph_replays_match_eager(hip):
             fakhip.call("fhip_q4k_matmul_group_f32", C.addressof(gw), C.addressof(gy),
                         C.addressof(gn), 3, x1.ptr, K, 1)
             fakhip.call("fhip_q4k_matmul_f32", w1, x40.ptr, outs["gemm"][k].ptr, 1024, K, 40)
+            fakhip.call("fhip_q4k_matmul_f32", ws, x40b.ptr, outs["gemm_split"][k].ptr, 1024, K4,
+                        40)
+            fakhip.call("fhip_q4k_matmul_f32", wt, x40.ptr, outs["gemm_tail"][k].ptr, NT, K, 40)
             fakhip.call("fhip_q8_matmul_f32", codes.ptr, scales.ptr, x1.ptr, outs["q8"][k].ptr, 320,
                         K, 1, 32)
             fakhip.call("fhip_q8_matmul_f32", codes.ptr, scales.ptr, x40.ptr, outs["q8b"][k].ptr,
@@ -60,8 +73,10 @@ def test_graph_replays_match_eager(hip):
 
         def set_x(seed):
             a1, a40 = synth.activations(1, K, seed), synth.activations(40, K, seed + 1)
+            a40b = synth.activations(40, K4, seed + 2)
             fakhip.call("fhip_h2d", x1.ptr, a1.ctypes.data, K * 4)
             fakhip.call("fhip_h2d", x40.ptr, a40.ctypes.data, 40 * K * 4)
+            fakhip.call("fhip_h2d", x40b.ptr, a40b.ctypes.data, 40 * K4 * 4)
 
         set_x(100)
         run(0)  # eager warm-up: sizes the workspace before capture
