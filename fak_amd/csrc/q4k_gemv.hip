@@ -631,9 +631,9 @@ I8Plan plan_i8(int ntiles, int K, bool swiglu) {
   I8Plan p{};
   const size_t ldsx = (size_t)nblk * op_bytes<MP>();
   i8_shape(ntiles, nblk, max_waves, ldsx, (size_t)64 * NT * 4, p.TW, p.KW);
-  // At most two tiles per CU: one workgroup of max_waves waves per CU (one tile, or two above
-  // one tile per CU), each wave streaming >= 1.5 records; more waves hide more of the record
-  // latency than longer per-wave streams do. Two to four tokens over 2..8 tiles per CU: eight
+  // At most two tiles per CU: one workgroup of up to max_waves waves per CU (one tile, or two
+  // above one tile per CU), each wave streaming >= 1.5 records (>= 3 for one token on a grid of
+  // half the CUs or more, see below). Two to four tokens over 2..8 tiles per CU: eight
   // one-wave tiles per workgroup, which share the (larger) quantization. Measured (us, this rule
   // / the rule above), one token: 3584 x 18944 13.2 / 13.8, 3584 x 3584 5.9 / 6.2, 4096 x 5120
   // 7.2 / 8.6, 5120 x 5120 7.4 / 8.7, 4608 x 3584 6.6 / 7.2, 8192 x 5120 8.2 / 10.0, 5120 x
@@ -644,7 +644,12 @@ I8Plan plan_i8(int ntiles, int K, bool swiglu) {
     if (ntiles <= 2 * cus) {
       p.TW = ntiles <= cus ? 1 : 2;
       p.KW = max_waves / p.TW;
-      while (p.KW > 1 && 2 * nblk < 3 * p.KW) p.KW /= 2;
+      // Records per wave: at least 1.5, and for one token on a grid of half the CUs or more at
+      // least 3 (4 against 8 K parts: 3584 x 3584 4.9-5.2 against 5.3 us, 4608 x 3584 5.7 / 6.6,
+      // 5120 x 5120 6.4 / 7.2, 6144 x 5120 6.6 / 7.4, 4096 x 5120 5.5 / 6.0; 512 x 3584, 32
+      // tiles, keeps 8 parts: 4.6 us either way; four tokens keep 8).
+      const int rec2 = MP == 1 && 2 * ntiles >= cus ? 6 : 3;  // twice the minimum
+      while (p.KW > 1 && 2 * nblk < rec2 * p.KW) p.KW /= 2;
     } else if (MP > 1 && ntiles <= 8 * cus) {
       p.TW = max_waves;
       p.KW = 1;
