@@ -164,7 +164,11 @@ __global__ void q6k_xprep_kernel(const float *__restrict__ x, int nblk,
 }
 
 // One token: workgroup = TW tiles x KW waves, wave (tile, part) streams super-blocks
-// [part nblk / KW, (part + 1) nblk / KW) of its tile with four records in flight.
+// [part nblk / KW, (part + 1) nblk / KW) of its tile with two records in flight. Two keep the
+// kernel at 92 VGPRs, five waves per SIMD; three records (112 VGPRs, four waves) measured 4%
+// slower and four (134, three waves: one 8-wave workgroup per CU) 8-20% slower (default shapes,
+// us for 2 / 3 / 4 records: 18944 x 3584 14.8 / 15.5 / 18.1, 25600 x 5120 20.9 / 21.9 / 25.4,
+// 14336 x 4096 10.7 / 11.2 / 11.4, 152064 x 3584 67.6 / 68.7 / 71.3).
 template <bool LX>
 __global__ __launch_bounds__(512) void q6k_gemv_kernel(const uint8_t *__restrict__ W,
                                                       const float *__restrict__ X,
@@ -198,7 +202,7 @@ __global__ __launch_bounds__(512) void q6k_gemv_kernel(const uint8_t *__restrict
     o.qh0 = ld_stream(rec + kQ6kQh + 256 * (gq & 1) + 16 * r);
     o.qh1 = ld_stream(rec + kQ6kQh + 512 + 256 * (gq & 1) + 16 * r);
   };
-  constexpr int PF = 4;
+  constexpr int PF = 2;
   Rec ring[PF];
 #pragma unroll
   for (int u = 0; u < PF; ++u)
@@ -299,11 +303,43 @@ struct Q6Plan {
   bool lds_x;
 };
 
+// Shape, measured one token at a time (us): up to one tile per CU, one tile of 8 waves (3584 x
+// 3584 5.2 against 5.6 with 4 waves, 4096 x 4096 5.5 / 5.9, 512 x 3584 4.5 / 4.9), each wave
+// streaming >= 1.5 records. Up to 8 tiles per CU: the workgroup of 1, 2 or 4 tiles (4, 4 or 2
+// waves each) whose grid puts the fewest tiles on the busiest CU, the widest on a tie (its
+// activation quantization serves more tiles): 18944 x 3584, 1184 tiles, 1 x 4 12.5 against
+// 4 x 2 15.5 (5 against 8 tiles); 11008 x 4096 1 x 4 9.8 / 10.3 (3 against 4); 14336 x 4096, 4
+// tiles each way, 4 x 2 / 2 x 4 11.1 against 1 x 4 11.6; 5120 x 25600 2 x 4 26.3 against 1 x 4
+// 28.1. Taller matrices take the Q4_K GEMV's rule (152064 x 3584: 2 x 2 68.7, 1 x 4 69.6).
+void q6_shape(int ntiles, int nblk, size_t ldsx, int &TW, int &KW) {
+  const int cus = cu_count() > 0 ? cu_count() : 256;
+  if (tuning().gemv_tw || tuning().gemv_kw || ntiles > 8 * cus) {
+    gemv_shape(ntiles, nblk, 8, ldsx, 64 * 4, TW, KW);
+    return;
+  }
+  if (ntiles <= cus) {
+    TW = 1;
+    KW = 8;
+  } else {
+    TW = 0;
+    int best = 1 << 30;
+    for (int tw = 1; tw <= 4; tw *= 2) {
+      const int load = tw * ceil_div(ceil_div(ntiles, tw), cus);
+      if (load <= best) {
+        best = load;
+        TW = tw;
+      }
+    }
+    KW = TW == 4 ? 2 : 4;
+  }
+  while (KW > 1 && 2 * nblk < 3 * KW) KW /= 2;
+}
+
 Q6Plan plan_q6k(int N, int K) {
   Q6Plan p{};
   const int nblk = K / 256, ntiles = q4k_tiles(N);
   p.ldsx = (size_t)nblk * kQ6Op;
-  gemv_shape(ntiles, nblk, 8, p.ldsx, 64 * 4, p.TW, p.KW);
+  q6_shape(ntiles, nblk, p.ldsx, p.TW, p.KW);
   p.redB = (size_t)p.TW * p.KW * 64 * 4;
   p.lds_x = p.ldsx + p.redB <= (size_t)lds_limit();
   return p;

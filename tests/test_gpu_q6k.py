@@ -62,7 +62,8 @@ def test_gemv_reference_fixture_exact(hip, oracle_mod):
 @pytest.mark.parametrize("out,in_,P", [(1536, 3584, 1), (3584, 18944, 1), (152, 4096, 5),
                                        (4096, 512, 3), (37, 256, 8), (17, 66048, 1),
                                        (152064, 3584, 1), (3584, 18944, 2), (3584, 18944, 16),
-                                       (1000, 2048, 13), (300, 768, 16)])
+                                       (1000, 2048, 13), (300, 768, 16), (18944, 3584, 1),
+                                       (5120, 4096, 1), (14336, 1024, 1), (8192, 768, 1)])
 def test_gemv_matches_oracle(hip, oracle_mod, out, in_, P):
     print(f"[case] q6k gemv out={out} in={in_} P={P}", flush=True)
     rng = np.random.default_rng(out + in_ + P)
