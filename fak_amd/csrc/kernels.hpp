@@ -123,6 +123,31 @@ __device__ __forceinline__ void digits4(float x0, float x1, float x2, float x3, 
       0x80808080u;
 }
 
+// digits4 with the scale given as the float s = 2^sh, for sh in [-126, 127] (s normal): one fma
+// per value. The product x s is exact in the fma, which then rounds x s + (1.5 2^23 + 128) once,
+// as the add after ldexpf(x, sh) does (where x 2^sh would be subnormal, |x 2^sh| < 2^-126 and
+// both round to the constant itself), so the digits are the same bits.
+__device__ __forceinline__ void digits4s(float x0, float x1, float x2, float x3, float s,
+                                         uint32_t &a, uint32_t &c) {
+  constexpr float kMagic = 12583040.f;  // 1.5 * 2^23 + 128
+  const uint32_t y0 = __float_as_uint(__builtin_fmaf(x0, s, kMagic));
+  const uint32_t y1 = __float_as_uint(__builtin_fmaf(x1, s, kMagic));
+  const uint32_t y2 = __float_as_uint(__builtin_fmaf(x2, s, kMagic));
+  const uint32_t y3 = __float_as_uint(__builtin_fmaf(x3, s, kMagic));
+  a = __builtin_amdgcn_perm(y1, y0, 0x0C0C0501u) | __builtin_amdgcn_perm(y3, y2, 0x05010C0Cu);
+  c = (__builtin_amdgcn_perm(y1, y0, 0x0C0C0400u) | __builtin_amdgcn_perm(y3, y2, 0x04000C0Cu)) ^
+      0x80808080u;
+}
+
+// Largest magnitude of four floats as a bit pattern: magnitudes order like their patterns, and a
+// NaN or an infinity gives a pattern >= 0x7F800000, so the integer maximum needs no NaN quieting
+// (fmaxf's) and the maximum of a block is order-free.
+__device__ __forceinline__ uint32_t absmax4_bits(float x0, float x1, float x2, float x3) {
+  const uint32_t m = 0x7FFFFFFFu;
+  return max(max(__float_as_uint(x0) & m, __float_as_uint(x1) & m),
+             max(__float_as_uint(x2) & m, __float_as_uint(x3) & m));
+}
+
 // Workgroup shape of the small-M GEMV kernels (TW tiles x KW waves; see q4k_gemv.hip).
 void gemv_shape(int ntiles, int nblk, int max_waves, size_t lds_fixed, size_t lds_per_wave,
                 int &TW, int &KW);

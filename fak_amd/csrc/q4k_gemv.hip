@@ -123,9 +123,11 @@ __device__ __forceinline__ float block_sum(const float (&v)[32]) {
 template <int MP>
 __device__ __forceinline__ void quant_vals(const float (&v)[32], int sig, int t,
                                            uint4 *__restrict__ A, float2 *__restrict__ ES) {
-  float amax = 0.f;
+  uint32_t mb = 0;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  for (int i = 0; i < 8; ++i)
+    mb = max(mb, absmax4_bits(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]));
+  const float amax = __uint_as_float(mb);  // a NaN when the block holds one
   const float s = block_sum(v);
   // e = 2^k, the smallest power of two with 127 e >= amax (amax = f 2^E, f in [0.5, 1)), so
   // x / e is exact and integer activations quantize without error. Non-finite blocks get
@@ -172,15 +174,22 @@ __device__ __forceinline__ void quant_block(const float *__restrict__ x, bool va
 // other quad of the eight, each pair added in either order: the sum commutes exactly).
 #define FHIP_DPP(v, ctrl) \
   __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, false))
+#define FHIP_DPP_U(v, ctrl) \
+  (uint32_t) __builtin_amdgcn_update_dpp(0, (int)(v), (ctrl), 0xF, 0xF, false)
 
+// The block maximum is taken on magnitude bit patterns (absmax4_bits): one DPP max per step, where
+// fmaxf needed a NaN-quieting max and a separate DPP move. The digits use one fma per value
+// (digits4s) unless a lane's scale 2^(8 - k) is not a normal float (blocks below ~2^-120, where
+// the wave takes ldexpf).
 template <int MP>
 __device__ __forceinline__ void quant_lanes(const float4 v, int lane, int t,
                                             uint4 *__restrict__ A, float2 *__restrict__ ES) {
   const int sig = lane >> 3, p = lane & 7;
-  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  amax = fmaxf(amax, FHIP_DPP(amax, 0xB1));   // quad_perm [1,0,3,2]: lane ^ 1
-  amax = fmaxf(amax, FHIP_DPP(amax, 0x4E));   // quad_perm [2,3,0,1]: lane ^ 2
-  amax = fmaxf(amax, FHIP_DPP(amax, 0x141));  // row_half_mirror: the other quad of the eight
+  uint32_t mb = absmax4_bits(v.x, v.y, v.z, v.w);
+  mb = max(mb, FHIP_DPP_U(mb, 0xB1));   // quad_perm [1,0,3,2]: lane ^ 1
+  mb = max(mb, FHIP_DPP_U(mb, 0x4E));   // quad_perm [2,3,0,1]: lane ^ 2
+  mb = max(mb, FHIP_DPP_U(mb, 0x141));  // row_half_mirror: the other quad of the eight
+  const float amax = __uint_as_float(mb);  // a NaN when the block holds one
   float sum = quad_sum(v.x, v.y, v.z, v.w);
   sum = sum + FHIP_DPP(sum, 0xB1);
   sum = sum + FHIP_DPP(sum, 0x4E);
@@ -192,7 +201,11 @@ __device__ __forceinline__ void quant_lanes(const float4 v, int lane, int t,
   if (!(amax <= 3.4e38f)) e = __builtin_nanf("");
   if (p == 0) ES[es_of<MP>(sig, t)] = make_float2(e, sum);
   uint32_t a, c;
-  digits4(v.x, v.y, v.z, v.w, 8 - k, a, c);
+  const int sh = 8 - k;
+  if (__builtin_expect(__builtin_amdgcn_ballot_w64(sh > 127) == 0, 1))
+    digits4s(v.x, v.y, v.z, v.w, ldexpf(1.f, sh), a, c);
+  else
+    digits4(v.x, v.y, v.z, v.w, sh, a, c);
   const int blk = blk_of<MP>(sig), g = p >> 1, half = p & 1;
   uint32_t *row0 = reinterpret_cast<uint32_t *>(A + ((size_t)blk * 16 + row_of<MP>(sig, t, 0)) * 4 + g);
   uint32_t *row1 = reinterpret_cast<uint32_t *>(A + ((size_t)blk * 16 + row_of<MP>(sig, t, 1)) * 4 + g);
@@ -398,7 +411,7 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
 #pragma unroll
         for (int i = 0; i < kPT; ++i)
           if (i < onb)
-            quant_lanes<MP>(t < M ? xv[t * kPT + i] : z, lane, t,
+            quant_lanes<MP>(MP == 1 || t < M ? xv[t * kPT + i] : z, lane, t,
                             const_cast<uint4 *>(A) + (size_t)(ob0 + i) * MP * 64,
                             const_cast<float2 *>(ES) + (size_t)(ob0 + i) * 8 * MP);
     } else if (xpre) {
@@ -408,7 +421,7 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
         if (c < nchunk) {
           const int t = chunk_tok(c), bl = c - t * nblk;
           const float4 z = {0.f, 0.f, 0.f, 0.f};
-          quant_lanes<MP>(t < M ? xv[j] : z, lane, t, const_cast<uint4 *>(A) + (size_t)bl * MP * 64,
+          quant_lanes<MP>(MP == 1 || t < M ? xv[j] : z, lane, t, const_cast<uint4 *>(A) + (size_t)bl * MP * 64,
                           const_cast<float2 *>(ES) + (size_t)bl * 8 * MP);
         }
       }
