@@ -294,7 +294,7 @@ def test_q4k_gemm_equals_gemv_per_token_within_tolerance(hip, oracle_mod):
 
 
 @pytest.mark.parametrize("out,in_,P", [(1536, 576, 1), (9, 512, 1), (17, 96, 3), (64, 1056, 16),
-                                       (100, 256, 40)])
+                                       (100, 256, 40), (37, 96, 1), (300, 1056, 1)])
 def test_q8_0_matmul(hip, oracle_mod, out, in_, P):
     print(f"[case] q8_0 out={out} in={in_} P={P}", flush=True)
     raw = synth.q8_0_weights(out, in_, seed=out * 3 + in_)
