@@ -731,8 +731,12 @@ int launch_i8(const GemvGroup &g, const float *X, int K, int M, bool swiglu, voi
   const bool exact = MP > 1 && ceil_div(nblk, p.KW) >= 12;
   if (p.lds_x) {
     if (swiglu) {
-      if (spread) FHIP_I8_LAUNCH(true, true, kXSpread, 2);
-      else FHIP_I8_LAUNCH(true, true, kXLate, 2);
+      if (spread) {
+        if (full) FHIP_I8_LAUNCH(true, true, kXSpread, MP == 1 ? 4 : 2);
+        else FHIP_I8_LAUNCH(true, true, kXSpread, 2);
+      } else {
+        FHIP_I8_LAUNCH(true, true, kXLate, 2);
+      }
     } else if (own) {
       if (full) FHIP_I8_LAUNCH(true, false, kXOwn, MP == 1 ? 4 : 2);
       else FHIP_I8_LAUNCH(true, false, kXOwn, 2);
