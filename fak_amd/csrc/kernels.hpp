@@ -89,21 +89,37 @@ __device__ __forceinline__ uint16_t ld_stream16(const void *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
 }
 
+// v + p[0] + p[stride] + ... + p[(N - 1) stride], in that order, every load issued first.
+template <int N, typename T>
+__device__ __forceinline__ T add_n(T v, const T *__restrict__ p, size_t stride) {
+  T q[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) q[j] = p[(size_t)j * stride];
+#pragma unroll
+  for (int j = 0; j < N; ++j) v = v + q[j];
+  return v;
+}
+
 // Ordered sum of K-range partial results: v (range 0) += p1[k * stride] for k = 0 .. count-1
-// (ranges 1 .. count), in that order. The loads go out eight at a time (indices clamped, so
-// every load is issued; a repeated one is not added): a loop of run-time length would wait for
-// each load before issuing the next.
+// (ranges 1 .. count), in that order. The loads go out eight at a time, the last group in a
+// straight-line block of exactly the remaining count (count is uniform over the launch, so the
+// choice is a scalar branch): a loop of run-time length would wait for each load before issuing
+// the next, and clamped indices re-issue the last range's load (6 repeats for two ranges).
 template <typename T>
 __device__ __forceinline__ T add_ranges(T v, const T *__restrict__ p1, size_t stride, int count) {
-  for (int k = 0; k < count; k += 8) {
-    T q[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) q[j] = p1[(size_t)min(k + j, count - 1) * stride];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (k + j < count) v = v + q[j];
+  int k = 0;
+  for (; k + 8 <= count; k += 8) v = add_n<8>(v, p1 + (size_t)k * stride, stride);
+  const T *p = p1 + (size_t)k * stride;
+  switch (count - k) {
+    case 1: return add_n<1>(v, p, stride);
+    case 2: return add_n<2>(v, p, stride);
+    case 3: return add_n<3>(v, p, stride);
+    case 4: return add_n<4>(v, p, stride);
+    case 5: return add_n<5>(v, p, stride);
+    case 6: return add_n<6>(v, p, stride);
+    case 7: return add_n<7>(v, p, stride);
+    default: return v;
   }
-  return v;
 }
 
 // Two-digit int8 activations: the digits of four values x at scale 2^sh (|x| 2^sh <= 32512): y = x 2^sh + (1.5 2^23 + 128)
