@@ -482,6 +482,27 @@ __global__ void gemv16_reduce_kernel(const float4 *__restrict__ part, float4 *__
   Y[id] = add_ranges(part[id], part + total4 + id, (size_t)total4, SK - 1);
 }
 
+// The same sum for up to kRangesAtOnce ranges, one output per thread in 64-thread workgroups,
+// every range's load issued before the first addition: with many ranges and few outputs (a long
+// down projection at a few tokens) the float4 form runs too few threads, each waiting on its
+// loads eight at a time. Same order, same bits.
+constexpr int kRangesAtOnce = 32;
+__global__ __launch_bounds__(64) void gemv16_reduce_wide_kernel(const float *__restrict__ part,
+                                                                float *__restrict__ Y, int SK,
+                                                                int total) {
+  const int id = blockIdx.x * 64 + threadIdx.x;
+  if (id >= total) return;
+  float q[kRangesAtOnce];
+#pragma unroll
+  for (int k = 0; k < kRangesAtOnce; ++k)
+    if (k < SK) q[k] = part[(size_t)k * total + id];
+  float v = q[0];
+#pragma unroll
+  for (int k = 1; k < kRangesAtOnce; ++k)
+    if (k < SK) v = v + q[k];
+  Y[id] = v;
+}
+
 }  // namespace
 
 // K ranges per call: ranges of 4 super-blocks when K allows it, else of 4 to 5 (the kernel
@@ -514,7 +535,9 @@ int launch_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M)
   FHIP_CHECK_LAUNCH("quant_gemv16_kernel");
   if (SK > 1) {
     const int tot = M * N;
-    if (tot % 4 == 0 && ((uintptr_t)Y & 15) == 0)
+    if (SK >= 8 && SK <= kRangesAtOnce)
+      gemv16_reduce_wide_kernel<<<ceil_div(tot, 64), 64, 0, stream()>>>(part, Y, SK, tot);
+    else if (tot % 4 == 0 && ((uintptr_t)Y & 15) == 0)
       gemv16_reduce_kernel<<<ceil_div(tot / 4, 256), 256, 0, stream()>>>(
           (const float4 *)part, (float4 *)Y, SK, tot / 4);
     else
