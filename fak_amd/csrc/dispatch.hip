@@ -7,8 +7,11 @@ using namespace fhip;
 
 namespace {
 
-// Up to this many tokens run the small-M GEMV kernels, more the prefill GEMM.
+// Up to kGemvMaxTokens tokens run the small-M GEMV kernels (decode, speculative verify); up to
+// kGemv32MaxTokens the same 32x32 kernel with one f16 operand row per token (small prefill
+// chunks, at the GEMM's activation precision); more the prefill GEMM.
 constexpr int kGemvMaxTokens = 16;
+constexpr int kGemv32MaxTokens = 32;
 
 int check_matmul(const char *who, const void *dPacked, const float *dX, const float *dY, int out,
                  int in, int P) {
@@ -28,12 +31,14 @@ int check_matmul(const char *who, const void *dPacked, const float *dX, const fl
 namespace fhip {
 int q4k_matmul_run(const void *dPacked, const float *dX, float *dY, int out, int in, int P) {
   if (P <= kGemvMaxTokens) return q4k_gemv(dPacked, dX, dY, out, in, P);
+  if (P <= kGemv32MaxTokens) return q4k_gemv32(dPacked, dX, dY, out, in, P);
   return q4k_gemm32(dPacked, dX, dY, out, in, P);
 }
 
 size_t q4k_matmul_ws_bytes(int out, int in, int P) {
   if (P <= 0) return 0;
   if (P <= kGemvMaxTokens) return q4k_gemv_ws_bytes(out, in, P);
+  if (P <= kGemv32MaxTokens) return gemv16_ws_bytes(0, out, in, P);
   return gemm32_ws_bytes(0, out, in, P);
 }
 }  // namespace fhip
@@ -79,7 +84,7 @@ int fhip_q4k_matmul_group_f32(const void *const *dPacked, float *const *dY, cons
   if (P == 0) return FHIP_OK;
   if (P <= kGemvMaxTokens) return q4k_gemv_group(g, dX, in, P);
   for (int i = 0; i < count; ++i)
-    if (int rc = q4k_gemm32(dPacked[i], dX, dY[i], out[i], in, P)) return rc;
+    if (int rc = q4k_matmul_run(dPacked[i], dX, dY[i], out[i], in, P)) return rc;
   return FHIP_OK;
 }
 

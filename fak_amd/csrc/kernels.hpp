@@ -37,8 +37,10 @@ struct GemvGroup {
 int q4k_gemv_group(const GemvGroup &g, const float *X, int K, int M);
 // 5..16 tokens (3..16 for K >= 24576) on the 32x32x16 MFMA with exact weight operands (q4k_gemv16.hip).
 int q4k_gemv16(const void *W, const float *X, float *Y, int N, int K, int M);
-// Scratch bytes of a q4k_gemv16 (fmt 0) / q6k_gemv16 (fmt 1) call.
+// Scratch bytes of a q4k_gemv16 (fmt 0) / q6k_gemv16 (fmt 1) / q4k_gemv32 call.
 size_t gemv16_ws_bytes(int fmt, int N, int K, int M);
+// 17..32 tokens on the same kernel with one f16 operand row per token (q4k_gemv16.hip).
+int q4k_gemv32(const void *W, const float *X, float *Y, int N, int K, int M);
 // The same for a tiled Q6_K weight.
 int q6k_gemv16(const void *W, const float *X, float *Y, int N, int K, int M);
 // Fused decode MLP pieces (1..4 tokens): the workspace a small-M call over `ntiles` tiles

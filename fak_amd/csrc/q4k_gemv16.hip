@@ -88,7 +88,10 @@ struct W16<1> {
   uint2 q[2][2][3];  // [K half hh][lane group h][ql a, ql b, qh]
 };
 
-template <int FMT>  // 0: Q4_K, 1: Q6_K
+// T32 (17..32 tokens, Q4_K): the 32 operand rows are 32 tokens, each the f16 of x / s_t with no
+// remainder row (the prefill GEMM's activation precision), the min term's rows S_s / 32 in f16;
+// one 32-row tile per wave (the second token's staging registers leave no room for two).
+template <int FMT, bool T32>  // FMT 0: Q4_K, 1: Q6_K
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void quant_gemv16_kernel(
     const uint8_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y,
     float *__restrict__ part, int N, int K, int M, int nblk, int ntiles, int SK) {
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int rb = blockIdx.x / SK, sp = blockIdx.x - rb * SK;
   const int kb0 = sp * nblk / SK, kb1 = (sp + 1) * nblk / SK;  // >= 1 super-block: SK <= nblk
   const int nb = kb1 - kb0;
-  constexpr int NT = tiles16<FMT>();              // 32-row MFMA tiles per wave
+  constexpr int NT = T32 ? 1 : tiles16<FMT>();    // 32-row MFMA tiles per wave
   constexpr int TWG = 8 * NT;                      // 16-row tiles per workgroup
   constexpr int kRec = FMT == 0 ? kQ4kRecord : kQ6kRecord;
   constexpr int kWL = FMT == 0 ? 10 : 14;          // record loads per super-block per lane
@@ -149,16 +152,64 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const bool xvalid = xt < M;
   const float4 *xrow = reinterpret_cast<const float4 *>(X + (size_t)(xvalid ? xt : 0) * K +
                                                         32 * xsb + 16 * xhalf);
+  // T32: the thread also stages token xt + 16 (operand row 16 + xt).
+  const bool xvalid1 = T32 && xt + 16 < M;
+  const float4 *xrow1 = reinterpret_cast<const float4 *>(X + (size_t)(xvalid1 ? xt + 16 : 0) * K +
+                                                         32 * xsb + 16 * xhalf);
+  constexpr int XV = T32 ? 8 : 4;  // float4 of activations per thread per super-block
   // Unconditional loads (tokens past M read token 0's row; store_x zeroes them): a load under
   // the token test sits in an exec-masked branch, and the merge after it made the compiler wait
   // for every load in flight, the records of the next super-block included.
-  auto load_x = [&](int b, float4 (&xv)[4]) {
+  auto load_x = [&](int b, float4 (&xv)[XV]) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) xv[q] = xrow[64 * (size_t)b + q];
+    if constexpr (T32) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) xv[4 + q] = xrow1[64 * (size_t)b + q];
+    }
   };
   // sk: the token's range scale exponent (0 for a range holding a NaN or an infinity: those
   // values reach the token's own operand rows only, and so only its outputs)
-  auto store_x = [&](float4 (&xv)[4], u32x4 *dst, int sk) {
+  // T32: both tokens' values as f16 rows xt and 16 + xt, sub-block sums S / 32 as f16 (the
+  // half-0 thread writes token xt's, the half-1 thread token xt + 16's).
+  auto store_x32 = [&](float4 (&xv)[XV], u32x4 *dst, int sk0, int sk1) {
+    float ps[2];
+#pragma unroll
+    for (int tk = 0; tk < 2; ++tk) {
+      const bool ok = tk ? xvalid1 : xvalid;
+      const int sk = tk ? sk1 : sk0;
+      float f[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 w = xv[4 * tk + q];
+        f[4 * q] = ok ? ldexpf(w.x, -sk) : 0.f;
+        f[4 * q + 1] = ok ? ldexpf(w.y, -sk) : 0.f;
+        f[4 * q + 2] = ok ? ldexpf(w.z, -sk) : 0.f;
+        f[4 * q + 3] = ok ? ldexpf(w.w, -sk) : 0.f;
+      }
+      ps[tk] = 0.f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) ps[tk] += f[k];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        f16x8 hv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hv[j] = (_Float16)f[8 * i + perm8(j)];
+        u32x4 *unit = dst + (2 * xsb + xhalf) * 64 + 32 * i;
+        unit[16 * tk + xt] = __builtin_bit_cast(u32x4, hv);
+      }
+    }
+    const float o0 = __shfl_xor(ps[0], 1), o1 = __shfl_xor(ps[1], 1);
+    const float S0 = (xhalf ? o0 + ps[0] : ps[0] + o0) * 0.03125f;
+    const float S1 = (xhalf ? o1 + ps[1] : ps[1] + o1) * 0.03125f;
+    _Float16 *su = reinterpret_cast<_Float16 *>(dst + 16 * 64);
+    const int j = perm8(xsb);
+    if (xhalf == 0)
+      su[xt * 8 + j] = (_Float16)S0;
+    else
+      su[(16 + xt) * 8 + j] = (_Float16)S1;
+  };
+  auto store_x = [&](float4 (&xv)[XV], u32x4 *dst, int sk) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       xv[q].x = xvalid ? ldexpf(xv[q].x, -sk) : 0.f;
@@ -214,13 +265,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int e = 0; e < 16; ++e) acc[t][e] = 0.f;
 
   W16<FMT> wr[2];
-  float4 xv[4];
-  auto absmax = [](uint32_t m, const float4 (&v)[4]) {
+  float4 xv[XV];
+  // Largest magnitude bit pattern of token tk's four float4 (tk = 1: the second token of T32).
+  auto absmax = [](uint32_t m, const float4 (&v)[XV], int tk = 0) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      m = max(max(max(m, __float_as_uint(v[q].x) & 0x7FFFFFFFu),
-                  __float_as_uint(v[q].y) & 0x7FFFFFFFu),
-              max(__float_as_uint(v[q].z) & 0x7FFFFFFFu, __float_as_uint(v[q].w) & 0x7FFFFFFFu));
+      m = max(max(max(m, __float_as_uint(v[4 * tk + q].x) & 0x7FFFFFFFu),
+                  __float_as_uint(v[4 * tk + q].y) & 0x7FFFFFFFu),
+              max(__float_as_uint(v[4 * tk + q].z) & 0x7FFFFFFFu,
+                  __float_as_uint(v[4 * tk + q].w) & 0x7FFFFFFFu));
     return m;
   };
   // Vector loads complete in issue order per CU: activation loads issued behind the first
@@ -229,8 +282,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // first stage), and a bare barrier holds every wave's records behind every wave's activation
   // loads; longer ranges read them after the records.
   constexpr int kPre = 5;
-  const bool xfirst = nb <= kPre;  // uniform over the workgroup
-  float4 xp[kPre][4];
+  const bool xfirst = !T32 && nb <= kPre;  // uniform over the workgroup
+  float4 xp[kPre][XV];
   if (xfirst) {
     // Straight-line (a range shorter than kPre repeats its last super-block, which leaves the
     // maximum unchanged), so the waits below count exactly.
@@ -256,7 +309,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // orders like the magnitudes; a NaN or an infinity makes it >= 0x7F800000): each stage lane
   // reads its 16 values of every super-block of the range, then the 16 lanes of the token
   // (adjacent: tid = 16 xt + ...) reduce with xor-swizzles (bit-mask mode, no address registers).
-  uint32_t mb = 0;
+  uint32_t mb = 0, mb1 = 0;
   if (xfirst) {
 #pragma unroll
     for (int j = 0; j < kPre; ++j) mb = absmax(mb, xp[j]);
@@ -264,19 +317,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int b = kb0; b < kb1; ++b) {
       load_x(b, xv);
       mb = absmax(mb, xv);
+      if (T32) mb1 = absmax(mb1, xv, 1);
     }
   }
-  mb = max(mb, (uint32_t)__builtin_amdgcn_ds_swizzle((int)mb, (1 << 10) | 0x1F));
-  mb = max(mb, (uint32_t)__builtin_amdgcn_ds_swizzle((int)mb, (2 << 10) | 0x1F));
-  mb = max(mb, (uint32_t)__builtin_amdgcn_ds_swizzle((int)mb, (4 << 10) | 0x1F));
-  mb = max(mb, (uint32_t)__builtin_amdgcn_ds_swizzle((int)mb, (8 << 10) | 0x1F));
-  const bool xfinite = mb < 0x7F800000u;
-  int xe = 0;
-  (void)frexpf(__uint_as_float(mb), &xe);
-  const int xsk = xfinite ? xe - 14 : 0;  // the range maximum / 2^xsk is in [2^13, 2^14)
-  __shared__ float tscale[16];
-  if (xsb == 0 && xhalf == 0)
-    tscale[xt] = !xfinite ? __builtin_nanf("") : mb ? ldexpf(1.f, xsk) : 1.f;
+  auto token_max = [](uint32_t m) {
+    m = max(m, (uint32_t)__builtin_amdgcn_ds_swizzle((int)m, (1 << 10) | 0x1F));
+    m = max(m, (uint32_t)__builtin_amdgcn_ds_swizzle((int)m, (2 << 10) | 0x1F));
+    m = max(m, (uint32_t)__builtin_amdgcn_ds_swizzle((int)m, (4 << 10) | 0x1F));
+    m = max(m, (uint32_t)__builtin_amdgcn_ds_swizzle((int)m, (8 << 10) | 0x1F));
+    return m;
+  };
+  // The range maximum / 2^sk is in [2^13, 2^14); a range holding a NaN or an infinity gets
+  // sk = 0 and the scale NaN.
+  auto range_exp = [](uint32_t m) {
+    int e = 0;
+    (void)frexpf(__uint_as_float(m), &e);
+    return m < 0x7F800000u ? e - 14 : 0;
+  };
+  auto range_scale = [](uint32_t m, int sk) {
+    return m >= 0x7F800000u ? __builtin_nanf("") : m ? ldexpf(1.f, sk) : 1.f;
+  };
+  mb = token_max(mb);
+  const int xsk = range_exp(mb);
+  __shared__ float tscale[T32 ? 32 : 16];
+  if (xsb == 0 && xhalf == 0) tscale[xt] = range_scale(mb, xsk);
+  int xsk1 = 0;
+  if constexpr (T32) {
+    mb1 = token_max(mb1);
+    xsk1 = range_exp(mb1);
+    if (xsb == 0 && xhalf == 0) tscale[16 + xt] = range_scale(mb1, xsk1);
+  }
   if (xfirst) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) xv[q] = xp[0][q];
@@ -287,7 +357,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int k = tid & 31;
     (tid < 32 ? As0 : As1)[16 * 64 + 32 + k] = u32x4{0u, 0u, 0u, 0u};
   }
-  store_x(xv, As0, xsk);
+  if constexpr (T32)
+    store_x32(xv, As0, xsk, xsk1);
+  else
+    store_x(xv, As0, xsk);
   // The first stage is in LDS; the first two super-blocks' records (2 kWL loads per lane) may
   // still be in flight: the first pass waits for its own.
   if (xfirst)
@@ -436,25 +509,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // work it would wait for the records of b + 1 too.)
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(wait_vm16(kWL));
-      store_x(xv, buf(u ^ 1), xsk);
+      if constexpr (T32)
+        store_x32(xv, buf(u ^ 1), xsk, xsk1);
+      else
+        store_x(xv, buf(u ^ 1), xsk);
       FHIP_LDS_BARRIER16(wait_vm16(kWL));
     }
   }
   // D layout: lane (kap, rho) holds column rho and operand rows 8 (e / 4) + 4 kap + e % 4:
   // e < 8 the hi rows of tokens 8 (e / 4) + 4 kap + e % 4, e + 8 the lo rows of the same tokens.
   // hi + lo rows, times the token's scale (the loop's barriers made tscale visible)
-  float v[NT][8];
+  // T32: every operand row is its own token (e = 0..15: rows 8 (e / 4) + 4 kap + e % 4).
+  constexpr int NV = T32 ? 16 : 8;
+  float v[NT][NV];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      v[t][e] = (acc[t][e] + acc[t][e + 8]) * tscale[8 * (e >> 2) + 4 * kap + (e & 3)];
+    for (int e = 0; e < NV; ++e)
+      v[t][e] = (T32 ? acc[t][e] : acc[t][e] + acc[t][e + 8]) *
+                tscale[8 * (e >> 2) + 4 * kap + (e & 3)];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int row = 16 * tile_of(t) + (lane & 15);  // recomputed: not kept live in the loop
     if (row >= N) continue;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < NV; ++e) {
       const int tok = 8 * (e >> 2) + 4 * kap + (e & 3);
       if (tok >= M) continue;
       if (SK == 1)
@@ -517,11 +596,12 @@ int gemv16_splits(int nblk) {
 }
 
 namespace {
-template <int FMT>
+template <int FMT, bool T32 = false>
 int launch_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
-  if (M < 1 || M > 16) return fail(FHIP_EINVAL, "gemv16: M=%d outside 1..16", M);
+  if (M < 1 || M > (T32 ? 32 : 16))
+    return fail(FHIP_EINVAL, "gemv16: M=%d outside 1..%d", M, T32 ? 32 : 16);
   const int nblk = K / 256, ntiles = q4k_tiles(N);
-  const int nrb = ceil_div(ntiles, 8 * tiles16<FMT>());
+  const int nrb = ceil_div(ntiles, 8 * (T32 ? 1 : tiles16<FMT>()));
   const int SK = gemv16_splits(nblk);
   float *part = nullptr;
   if (SK > 1) {
@@ -530,7 +610,7 @@ int launch_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M)
     if (int rc = check_disjoint("gemv16", X, (size_t)M * K * 4, part, (size_t)SK * M * N * 4))
       return rc;
   }
-  quant_gemv16_kernel<FMT><<<nrb * SK, 256, 0, stream()>>>((const uint8_t *)Wv, X, Y, part, N, K,
+  quant_gemv16_kernel<FMT, T32><<<nrb * SK, 256, 0, stream()>>>((const uint8_t *)Wv, X, Y, part, N, K,
                                                             M, nblk, ntiles, SK);
   FHIP_CHECK_LAUNCH("quant_gemv16_kernel");
   if (SK > 1) {
@@ -560,6 +640,13 @@ int q4k_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
 
 int q6k_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
   return launch_gemv16<1>(Wv, X, Y, N, K, M);
+}
+
+// 17..32 tokens of a Q4_K matmul, at the prefill GEMM's activation precision (f16 of x / s per
+// token and K range): a chunk of a few tens of tokens costs about what 16 do here, where the
+// 128-token tile of the prefill GEMM costs nearly what 128 do.
+int q4k_gemv32(const void *Wv, const float *X, float *Y, int N, int K, int M) {
+  return launch_gemv16<0, true>(Wv, X, Y, N, K, M);
 }
 
 }  // namespace fhip

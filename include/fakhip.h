@@ -126,7 +126,8 @@ void *fhip_q4k_upload(const uint8_t *hRaw, int out, int in);
  * replacement for fcuda_q4k_matmul_f32 (internal/compute/cuda_backend.h:120), which took the
  * raw bytes; this one takes the tiled buffer fhip_q4k_upload / fhip_q4k_repack produced and
  * returns FHIP_EINVAL for anything else (see Conventions).
- * P <= 16 runs the small-M GEMV (decode / speculative verify); larger P runs the MFMA GEMM.
+ * P <= 16 runs the small-M GEMV (decode / speculative verify); 17 <= P <= 32 the same 32x32
+ * kernel with one f16 activation row per token (small prefill chunks); larger P the MFMA GEMM.
  * Error bound vs the f32 reference: GEMV max|dY|/RMS(Y) <= 1e-3, GEMM <= 1e-2. */
 int fhip_q4k_matmul_f32(const void *dPacked, const float *dX, float *dY, int out, int in,
                         int P);

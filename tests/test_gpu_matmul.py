@@ -2,7 +2,8 @@
 inputs, at the reference's tolerances (metric of internal/model/quant_q4k_test.go:140-158):
 
   GEMV (P <= 16, f32-accumulate)  max|dY|/RMS(Y_ref) <= 1e-3
-  GEMM (P > 16, f16 MFMA)         max|dY|/RMS(Y_ref) <= 1e-2
+  P > 16 (f16 MFMA: 17..32 on the small-M kernel's f16 form, more on the prefill GEMM)
+                                  max|dY|/RMS(Y_ref) <= 1e-2
 
 Shapes: the five workloads (Q8_0 576->1536; Q4_K 3584->18944 and 18944->3584; prefill
 M=128/512/2048 at 3584->18944; 27B-class 5120<->25600 at M=1,4,8,16) plus small/ragged shapes
@@ -193,10 +194,35 @@ def test_q4k_small_m_27b(hip, oracle_mod, out, in_, P):
     _check_q4k(oracle_mod, out, in_, P, seed=77 + P + out, tol=GEMV_TOL)
 
 
-@pytest.mark.parametrize("out,in_,P", [(256, 512, 17), (300, 768, 40), (512, 1024, 128),
+@pytest.mark.parametrize("out,in_,P", [(256, 512, 33), (300, 768, 40), (512, 1024, 128),
                                        (1000, 2048, 200), (64, 256, 1000)])
 def test_q4k_gemm_small_shapes(hip, oracle_mod, out, in_, P):
     _check_q4k(oracle_mod, out, in_, P, seed=out + in_ + P, tol=GEMM_TOL)
+
+
+@pytest.mark.parametrize("out,in_,P", [(18944, 3584, 17), (18944, 3584, 24), (3584, 18944, 32),
+                                       (5120, 25600, 20), (1000, 2048, 19), (300, 768, 32),
+                                       (16, 256, 31), (100, 1024, 25)])
+def test_q4k_small_prefill_17_to_32(hip, oracle_mod, out, in_, P):
+    """17..32 tokens on the 32x32 small-M kernel with one f16 operand row per token (K split in
+    ranges at the long shapes): every output against the oracle at the GEMM bound."""
+    rows = 256 if out * in_ > 4096 * 4096 else None
+    e = _check_q4k(oracle_mod, out, in_, P, seed=3 * out + in_ + P, tol=GEMM_TOL, rows=rows)
+    assert e <= 2e-3, e  # f16 activations under a per-token power-of-two scale: ~1e-3
+
+
+@pytest.mark.parametrize("pattern", ["big", "tiny", "mixed", "outlier"])
+def test_q4k_small_prefill_activation_scales(hip, oracle_mod, pattern):
+    from tests.gpu_util import rel_err_rows, scaled_activations
+    out, in_, P = 512, 2048, 24
+    print(f"[case] q4k 17..32 scales out={out} in={in_} P={P} {pattern}", flush=True)
+    raw = synth.q4k_weights(out, in_, seed=out + P)
+    X = scaled_activations(P, in_, 3 * P + 1, pattern)
+    Y = q4k_matmul(raw, out, in_, X, P)
+    ref = oracle_mod.q4k_gemm(raw, out, in_, X, P, workers=16)
+    e = rel_err_rows(Y, ref)
+    print(f"    per-row max|d|/RMS = {e:.3e}", flush=True)
+    assert e <= GEMM_TOL, e
 
 
 @pytest.mark.parametrize("P", [128, 512, 2048])
