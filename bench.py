@@ -15,7 +15,8 @@ The other workloads are reported under "workloads", each with its error against 
 back to back, and one graph of 300 launches over 300 weight copies), the prefill GEMM at
 M=128/512/2048 (TFLOP/s of calls launched back to back, like the GEMV headline, vs the
 2.5 PFLOP/s dense f16 MFMA peak; the per-call figure, with the host waiting on an event pair
-around every call, is reported beside it), the 28-layer Qwen2.5-7B decode
+around every call, is reported beside it), the small-M -> MFMA crossover on the same shape
+(1..128 tokens, each token count's route named), the 28-layer Qwen2.5-7B decode
 matmul set (tokens/s bound by matmul time, with q/k/v and gate/up as group launches; one graph
 per token and one launch per matmul beside it) and the 27B-class small-M verify widths.
 
@@ -147,6 +148,29 @@ def sample_rows(raw, n, k, rows):
     rb = (k // 256) * 144
     sel = np.concatenate([np.arange(0, rows // 2), np.arange(n - rows // 2, n)])
     return np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel]), sel
+
+
+def bench_crossover(steps, warmup, ev, tokens=(1, 2, 4, 8, 16, 17, 24, 32, 48, 64, 128)):
+    """The small-M -> MFMA crossover on the C3 shape (K=3584 -> N=18944): every route
+    fhip_q4k_matmul_f32 takes by token count (int8 GEMV 1..4, the 32x32 hi/lo GEMV 5..16, its
+    f16 form 17..32, the prefill GEMM beyond), back to back over the rotating weight copies."""
+    n, k = 18944, 3584
+    w = Weight("q4k", n, k, 3, copies_for(q4k_bytes(n, k)))
+    out = []
+    for M in tokens:
+        X = synth.activations(M, k, 4)
+        xb, yb = Buf(X.nbytes, X), Buf(M * n * 4)
+        ms, _ = time_calls([("fhip_q4k_matmul_f32",
+                             lambda i: (w.ptrs[i % len(w.ptrs)], xb.ptr, yb.ptr, n, k, M))],
+                           steps, warmup, ev)
+        route = ("int8 GEMV" if M <= 4 else "32x32 GEMV, hi/lo f16" if M <= 16 else
+                 "32x32 GEMV, f16" if M <= 32 else "prefill GEMM")
+        out.append({"M": M, "route": route, "us_back_to_back": 1e3 * ms,
+                    "GBs": q4k_bytes(n, k) / (ms * 1e6),
+                    "TFLOPs": 2.0 * M * n * k / (ms * 1e-3) / 1e12})
+        xb.free(), yb.free()
+    w.free()
+    return out
 
 
 def time_calls(calls, steps, warmup, ev):
@@ -745,6 +769,9 @@ def main():
             print(f"[bench] C3 M={M} {r['us_back_to_back']:.1f} us {r['TFLOPs']:.0f} TFLOP/s",
                   file=sys.stderr, flush=True)
         wl["c3_prefill_gemm"] = c3
+        wl["c3_crossover"] = bench_crossover(steps, 3, ev)
+        print(f"[bench] C3 crossover {[round(r['us_back_to_back'], 1) for r in wl['c3_crossover']]} us",
+              file=sys.stderr, flush=True)
         wl["c4_decode_stack"], c4_in = bench_decode_stack(max(5, args.steps // 20), 2, ev)
         print(f"[bench] C4 {wl['c4_decode_stack']['tok_per_s']:.0f} tok/s", file=sys.stderr,
               flush=True)
