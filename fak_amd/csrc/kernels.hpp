@@ -41,6 +41,7 @@ int q4k_gemv16(const void *W, const float *X, float *Y, int N, int K, int M);
 size_t gemv16_ws_bytes(int fmt, int N, int K, int M);
 // 17..32 tokens on the same kernel with one f16 operand row per token (q4k_gemv16.hip).
 int q4k_gemv32(const void *W, const float *X, float *Y, int N, int K, int M);
+int q6k_gemv32(const void *W, const float *X, float *Y, int N, int K, int M);
 // The same for a tiled Q6_K weight.
 int q6k_gemv16(const void *W, const float *X, float *Y, int N, int K, int M);
 // Fused decode MLP pieces (1..4 tokens): the workspace a small-M call over `ntiles` tiles

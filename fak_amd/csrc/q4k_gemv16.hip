@@ -88,9 +88,10 @@ struct W16<1> {
   uint2 q[2][2][3];  // [K half hh][lane group h][ql a, ql b, qh]
 };
 
-// T32 (17..32 tokens, Q4_K): the 32 operand rows are 32 tokens, each the f16 of x / s_t with no
-// remainder row (the prefill GEMM's activation precision), the min term's rows S_s / 32 in f16;
-// one 32-row tile per wave (the second token's staging registers leave no room for two).
+// T32 (17..32 tokens): the 32 operand rows are 32 tokens, each the f16 of x / s_t with no
+// remainder row (the prefill GEMM's activation precision), the Q4_K min term's rows S_s / 32 in
+// f16; one 32-row tile per wave (for Q4_K the second token's staging registers leave no room for
+// two; Q6_K always runs one).
 template <int FMT, bool T32>  // FMT 0: Q4_K, 1: Q6_K
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void quant_gemv16_kernel(
     const uint8_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y,
@@ -647,6 +648,10 @@ int q6k_gemv16(const void *Wv, const float *X, float *Y, int N, int K, int M) {
 // 128-token tile of the prefill GEMM costs nearly what 128 do.
 int q4k_gemv32(const void *Wv, const float *X, float *Y, int N, int K, int M) {
   return launch_gemv16<0, true>(Wv, X, Y, N, K, M);
+}
+
+int q6k_gemv32(const void *Wv, const float *X, float *Y, int N, int K, int M) {
+  return launch_gemv16<1, true>(Wv, X, Y, N, K, M);
 }
 
 }  // namespace fhip

@@ -370,17 +370,20 @@ int launch_q6k_gemv(const uint8_t *W, const float *x, float *y, int N, int K) {
 }  // namespace
 
 // Q6_K matmul on the tiled layout: one token on the int8 GEMV above, 2..16 tokens in one launch
-// of the 32x32 MFMA kernel of q4k_gemv16.hip (max|dY|/RMS <= 1e-3), more through the f16 MFMA
-// prefill GEMM (q4k_gemm32.hip, <= 1e-2).
+// of the 32x32 MFMA kernel of q4k_gemv16.hip (max|dY|/RMS <= 1e-3), 17..32 on that kernel's f16
+// form (one operand row per token) and more through the f16 MFMA prefill GEMM (q4k_gemm32.hip),
+// both within the GEMM bound 1e-2.
 size_t q6k_gemv_ws_bytes(int N, int K, int M) {
-  if (M > 16) return gemm32_ws_bytes(1, N, K, M);
+  if (M > 32) return gemm32_ws_bytes(1, N, K, M);
+  if (M > 16) return gemv16_ws_bytes(1, N, K, M);
   if (M > 1) return gemv16_ws_bytes(1, N, K, M);
   const Q6Plan p = plan_q6k(N, K);
   return p.lds_x ? 0 : p.ldsx;
 }
 
 int q6k_gemv(const void *dW, const float *dX, float *dY, int out, int in, int P) {
-  if (P > 16) return q6k_gemm32(dW, dX, dY, out, in, P);
+  if (P > 32) return q6k_gemm32(dW, dX, dY, out, in, P);
+  if (P > 16) return q6k_gemv32(dW, dX, dY, out, in, P);
   if (P > 1) return q6k_gemv16(dW, dX, dY, out, in, P);
   return launch_q6k_gemv((const uint8_t *)dW, dX, dY, out, in);
 }
