@@ -256,7 +256,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
                                                          const uint4 *__restrict__ xa,
                                                          const float *__restrict__ tscale,
                                                          float *__restrict__ Y, int N, int M,
-                                                         int nblk, int ntiles, int MTG) {
+                                                         int nblk, int ntiles, int MTG, int F0,
+                                                         int S, int R, float *__restrict__ part) {
   using F = GemmFmt<FMT>;
   constexpr int kRec = F::kRec, kWU = F::kWU, kWPT = F::kWPT, kWUP = F::kWUP;
   __shared__ u32x4 As[2][kAU];
@@ -266,7 +267,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
   const int kap = lane >> 5, rho = lane & 31;
-  const int mg = blockIdx.x % MTG, ng = blockIdx.x / MTG;
+  // Workgroup -> (tile task, K range sp of ns), as in q4k_gemm32s_kernel: the first F0
+  // workgroups run whole tiles, the next R * S the last R tiles in S K ranges each; range 0
+  // writes Y, the others their partial sums for gemm32_reduce_kernel.
+  const int w = blockIdx.x;
+  const bool split = w >= F0;
+  const int pw = split ? w - F0 : 0;
+  const int task = split ? F0 + pw / S : w, sp = split ? pw % S : 0, ns = split ? S : 1;
+  const int mg = task % MTG, ng = task / MTG;
+  const int kb0 = sp * nblk / ns, kb1 = (sp + 1) * nblk / ns;  // >= 1 super-block: S <= nblk
   const int nq = nblk * 16;
   const Magic K = magic_consts();
 
@@ -323,8 +332,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   u32x4 areg[4], wreg[kWPT];
-  LOAD_W(0, wreg)
-  LOAD_A(0, areg)
+  LOAD_W(kb0, wreg)
+  LOAD_A(4 * kb0, areg)
   if (tid < kBM) ts_lds[tid] = tscale[kBM * mg + tid];  // tscale holds MTG * kBM entries
   STORE_W(0, wreg)
 #pragma unroll
@@ -335,8 +344,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   // byte offset of its row inside a record.
   const int Tl0 = 4 * wn + (rho >> 4), Tl1 = Tl0 + 2;
   const int r16 = rho & 15;
-  const int nst = nblk * 4;
-  for (int b = 0; b < nblk; ++b) {
+  const int nst = kb1 * 4;
+  for (int b = kb0; b < kb1; ++b) {
     const int wb = NWB == 2 ? (b & 1) : 0;
     const unsigned char *wbase = reinterpret_cast<const unsigned char *>(Ws[wb]);
     RowScales rs[2];
@@ -353,7 +362,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
         d6[t] = (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t *>(rec + kQ6kD + 2 * r16));
       }
     }
-    const bool more = b + 1 < nblk;
+    const bool more = b + 1 < kb1;
     if (more) {
       LOAD_W(b + 1, wreg)
     }
@@ -450,7 +459,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int tok = t0 + 8 * (v >> 2) + (v & 3);
-        if (tok < M) Y[(size_t)tok * N + o] = acc[i][t][v] * sc[v];
+        if (tok >= M) continue;
+        const float val = acc[i][t][v] * sc[v];
+        if (sp == 0)
+          Y[(size_t)tok * N + o] = val;
+        else
+          part[((size_t)(sp - 1) * R + (task - F0)) * kTileElems + (tok - kBM * mg) * 128 +
+               (o - 128 * ng)] = val;
       }
     }
   }
@@ -728,8 +743,10 @@ GemmPlan plan_gemm32(int fmt, int N, int K, int M) {
   p.F = p.tasks;
   p.S = 1;
   p.R = 0;
-  if (p.form != 1) {
-    // K splits of the staged kernel (partial sums added in range order):
+  {  // every form and format (the 2x2 form takes the same ranges, so the forms stay bit-identical)
+    // K splits (partial sums added in range order), for both forms: without them the 2x2 form
+    // ran a 3584 x 18944 Q6_K down projection on 28 workgroups at 64..128 tokens (315 us, 55-60
+    // with the split):
     //  * a grid smaller than the GPU (the 3584-row down projection, or 128 tokens) splits every
     //    tile into as many ranges as keep the grid within two workgroups per CU (at least 4
     //    super-blocks each): a third workgroup on some CUs sets the time (down projection at
@@ -768,7 +785,7 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
   const int nblk = K / 256;
   const int ntiles = q4k_tiles(N);
   const GemmPlan p = plan_gemm32(fmt, N, K, M);
-  const int MTG = p.MTG, grid = p.tasks;
+  const int MTG = p.MTG;
   unsigned char *ws = (unsigned char *)workspace(p.xab + p.tsb + p.pb);
   if (!ws) return FHIP_ENOMEM;
   if (int rc = check_disjoint("gemm32", X, (size_t)M * K * 4, ws, p.xab + p.tsb + p.pb)) return rc;
@@ -778,15 +795,7 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
   launch_xprep(X, M, K, MTG, xa, ts);
   FHIP_CHECK_LAUNCH("gemm32_xprep_kernel");
   const uint8_t *W = (const uint8_t *)Wv;
-  if (fmt == 1) {  // 60 KB of LDS with one weight buffer: two workgroups per CU
-    quant_gemm32_kernel<1, 1, 2><<<grid, 256, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles, MTG);
-    FHIP_CHECK_LAUNCH("quant_gemm32_kernel");
-    return FHIP_OK;
-  }
-  if (p.form != 1) {
-    q4k_gemm32s_kernel<<<p.F + p.R * p.S, 64 * kGemmWaves, 0, stream()>>>(
-        W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
-    FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
+  auto reduce = [&]() -> int {
     if (p.R) {
       const long long quads = (long long)p.R * (kTileElems / 4);
       gemm32_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, stream()>>>(
@@ -794,13 +803,28 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
       FHIP_CHECK_LAUNCH("gemm32_reduce_kernel");
     }
     return FHIP_OK;
+  };
+  const int grid2 = p.F + p.R * p.S;
+  if (fmt == 1) {  // 60 KB of LDS with one weight buffer: two workgroups per CU
+    quant_gemm32_kernel<1, 1, 2><<<grid2, 256, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles,
+                                                               MTG, p.F, p.S, p.R, part);
+    FHIP_CHECK_LAUNCH("quant_gemm32_kernel");
+    return reduce();
+  }
+  if (p.form != 1) {
+    q4k_gemm32s_kernel<<<grid2, 64 * kGemmWaves, 0, stream()>>>(
+        W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
+    FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
+    return reduce();
   }
   if (tuning().gemm32_nwb == 2)
-    quant_gemm32_kernel<0, 2, 2><<<grid, 256, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles, MTG);
+    quant_gemm32_kernel<0, 2, 2><<<grid2, 256, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles,
+                                                               MTG, p.F, p.S, p.R, part);
   else
-    quant_gemm32_kernel<0, 1, 3><<<grid, 256, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles, MTG);
+    quant_gemm32_kernel<0, 1, 3><<<grid2, 256, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles,
+                                                               MTG, p.F, p.S, p.R, part);
   FHIP_CHECK_LAUNCH("quant_gemm32_kernel");
-  return FHIP_OK;
+  return reduce();
 }
 }  // namespace
 

@@ -242,12 +242,17 @@ def test_q4k_gemm_forms_bit_identical(hip, oracle_mod, monkeypatch, out, in_, P)
     print(f"[case] gemm forms out={out} in={in_} P={P}", flush=True)
     raw = synth.q4k_weights(out, in_, seed=out + 3 * P)
     X = synth.activations(P, in_, seed=P + 5)
-    with knobs(monkeypatch, FAK_HIP_GEMM32_FORM=1):
+    # without a K split, and with the K ranges the launch rule picks (the same for both forms,
+    # added by the same ordered reduce)
+    with knobs(monkeypatch, FAK_HIP_GEMM32_FORM=1, FAK_HIP_GEMM32_SK=1):
         Y1 = q4k_matmul(raw, out, in_, X, P)
-    # the default form with no K split: the same summation order
     with knobs(monkeypatch, FAK_HIP_GEMM32_SK=1):
         Y3 = q4k_matmul(raw, out, in_, X, P)
     assert np.array_equal(Y1.view(np.uint32), Y3.view(np.uint32))
+    with knobs(monkeypatch, FAK_HIP_GEMM32_FORM=1):
+        Y2 = q4k_matmul(raw, out, in_, X, P)
+    Y4 = q4k_matmul(raw, out, in_, X, P)
+    assert np.array_equal(Y2.view(np.uint32), Y4.view(np.uint32))
     if out > 4096:
         rb = (in_ // 256) * 144
         sel = np.concatenate([np.arange(0, 128), np.arange(out - 128, out)])
