@@ -16,7 +16,8 @@ back to back, and one graph of 300 launches over 300 weight copies), the prefill
 M=128/512/2048 (TFLOP/s of calls launched back to back, like the GEMV headline, vs the
 2.5 PFLOP/s dense f16 MFMA peak; the per-call figure, with the host waiting on an event pair
 around every call, is reported beside it), the small-M -> MFMA crossover on the same shape
-(1..128 tokens, each token count's route named), the 28-layer Qwen2.5-7B decode
+(1..128 tokens, each token count's route named), the Q6_K GEMV and Q6_K prefill (32 / 128 / 512
+tokens) on the 7B FFN shapes, the 28-layer Qwen2.5-7B decode
 matmul set (tokens/s bound by matmul time, with q/k/v and gate/up as group launches; one graph
 per token and one launch per matmul beside it) and the 27B-class small-M verify widths.
 
@@ -392,8 +393,9 @@ def bench_int8_route(steps, warmup, ev):
     return out
 
 
-def bench_q6k(steps, warmup, ev):
-    """GGUF Q6_K GEMV (the q4_k_m ffn_down / lm_head quant) on the 7B FFN shapes, M=1."""
+def bench_q6k(steps, warmup, ev, tokens=(1,)):
+    """GGUF Q6_K matmul (the q4_k_m ffn_down / lm_head quant) on the 7B FFN shapes: the GEMV at
+    M=1, and with tokens=(...) each token count back to back (M > 32: the prefill GEMM)."""
     out = []
     for n, k in ((3584, 18944), (18944, 3584)):
         rng = np.random.default_rng(n)
@@ -409,14 +411,20 @@ def bench_q6k(steps, warmup, ev):
             p = fakhip.alloc_call("fhip_malloc", dev_bytes)
             fakhip.call("fhip_d2d", p, p0, dev_bytes)
             ptrs.append(p)
-        x = synth.activations(1, k, 5)
-        xb, yb = Buf(x.nbytes, x), Buf(n * 4)
-        call = ("fhip_q6k_matmul_f32", lambda i: (ptrs[i % len(ptrs)], xb.ptr, yb.ptr, n, k, 1))
-        us = 1e3 * time_one(call, steps, warmup, ev)
-        alg = nbytes + 4 * (n + k)
-        out.append({"N": n, "K": k, "us_per_call": round(us, 3), "GBs": round(alg / (us * 1e3), 1),
-                    "pct_hbm_peak": round(100.0 * alg / (us * 1e3) / HBM_PEAK_GBS, 1)})
-        xb.free(), yb.free()
+        for M in tokens:
+            x = synth.activations(M, k, 5)
+            xb, yb = Buf(x.nbytes, x), Buf(M * n * 4)
+            call = ("fhip_q6k_matmul_f32",
+                    lambda i: (ptrs[i % len(ptrs)], xb.ptr, yb.ptr, n, k, M))
+            us = 1e3 * time_one(call, steps, warmup, ev)
+            alg = nbytes + 4 * M * (n + k)
+            r = {"N": n, "K": k, "M": M, "us_per_call": round(us, 3),
+                 "GBs": round(alg / (us * 1e3), 1),
+                 "pct_hbm_peak": round(100.0 * alg / (us * 1e3) / HBM_PEAK_GBS, 1)}
+            if M > 1:
+                r["TFLOPs"] = round(2.0 * M * n * k / (us * 1e-6) / 1e12, 1)
+            out.append(r)
+            xb.free(), yb.free()
         for p in ptrs:
             lib.fhip_free(p)
     return out
@@ -780,6 +788,7 @@ def main():
               file=sys.stderr, flush=True)
         wl["int8_route"] = bench_int8_route(steps, 3, ev)
         wl["q6k_gemv"] = bench_q6k(steps, 3, ev)
+        wl["q6k_prefill"] = bench_q6k(max(5, steps // 4), 2, ev, tokens=(32, 128, 512))
         wl["fused_mlp"] = bench_mlp(steps, 3, ev)
         line["workloads"] = wl
     if not args.no_cpu:
