@@ -158,6 +158,48 @@ __device__ __forceinline__ void digits4s(float x0, float x1, float x2, float x3,
       0x80808080u;
 }
 
+// Three-digit int8 activations: the digits of four values x at scale 2^sh with |x 2^sh| <=
+// 63 * 2^16. y = x 2^sh + (1.5 2^23 + 32896) lies in [2^23, 2^24), where floats are the
+// integers, so the add rounds x 2^sh half to even exactly as rint, giving T, and the low 23 bits
+// of y hold 2^22 + T + 32896 = 2^22 + 65536 q1 + 256 (q2 + 128) + (q3 + 128) with q2, q3 in
+// [-128, 127] and q1 in [-63, 63]. Byte 0 of y is q3 ^ 0x80, byte 1 q2 ^ 0x80 and byte 2 q1 + 64
+// (in [1, 127]); q1 + q2 / 256 + q3 / 65536 = T / 65536 exactly. a gathers the four q1, b the
+// four q2, c the four q3 (value i in byte i), each as a two's complement byte.
+__device__ __forceinline__ void digits3_pack(uint32_t y0, uint32_t y1, uint32_t y2, uint32_t y3,
+                                             uint32_t &a, uint32_t &b, uint32_t &c) {
+  // Bytes 0 and 1 of the four words, transposed in two steps: t01 = {y0.0, y1.0, y0.1, y1.1},
+  // t23 = {y2.0, y3.0, y2.1, y3.1}.
+  const uint32_t t01 = __builtin_amdgcn_perm(y1, y0, 0x05010400u);
+  const uint32_t t23 = __builtin_amdgcn_perm(y3, y2, 0x05010400u);
+  c = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
+  b = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
+  // q1 + 64 -> q1: flipping bit 6 gives q1 for q1 >= 0 and q1 + 128 for q1 < 0 (bit 6 then set),
+  // and copying bit 6 into bit 7 turns the latter into the byte q1 + 256.
+  const uint32_t w =
+      (__builtin_amdgcn_perm(y1, y0, 0x0C0C0602u) | __builtin_amdgcn_perm(y3, y2, 0x06020C0Cu)) ^
+      0x40404040u;
+  a = w | ((w << 1) & 0x80808080u);
+}
+constexpr float kMagic3 = 12615808.f;  // 1.5 * 2^23 + 32896
+
+__device__ __forceinline__ void digits3(float x0, float x1, float x2, float x3, int sh,
+                                        uint32_t &a, uint32_t &b, uint32_t &c) {
+  digits3_pack(__float_as_uint(ldexpf(x0, sh) + kMagic3), __float_as_uint(ldexpf(x1, sh) + kMagic3),
+               __float_as_uint(ldexpf(x2, sh) + kMagic3), __float_as_uint(ldexpf(x3, sh) + kMagic3),
+               a, b, c);
+}
+
+// digits3 with the scale given as the float s = 2^sh (s normal): one fma per value, the same
+// bits as digits3 (the fma rounds the exact product plus the constant once, as the add after
+// ldexpf does).
+__device__ __forceinline__ void digits3s(float x0, float x1, float x2, float x3, float s,
+                                         uint32_t &a, uint32_t &b, uint32_t &c) {
+  digits3_pack(__float_as_uint(__builtin_fmaf(x0, s, kMagic3)),
+               __float_as_uint(__builtin_fmaf(x1, s, kMagic3)),
+               __float_as_uint(__builtin_fmaf(x2, s, kMagic3)),
+               __float_as_uint(__builtin_fmaf(x3, s, kMagic3)), a, b, c);
+}
+
 // Largest magnitude of four floats as a bit pattern: magnitudes order like their patterns, and a
 // NaN or an infinity gives a pattern >= 0x7F800000, so the integer maximum needs no NaN quieting
 // (fmaxf's) and the maximum of a block is order-free.

@@ -9,20 +9,25 @@
 // and the integer-weight dot sum_k n_k x_k runs on the int8 MFMA v_mfma_i32_16x16x64_i8:
 //   * weight operand: the 4-bit codes n (0..15) are int8 values as they stand; a dword of 8
 //     nibbles becomes two int8x4 words, `q & 0x0F0F0F0F` and `(q >> 4) & 0x0F0F0F0F`.
-//   * activation operand: every 32-value sub-block of a token is quantized to two int8 digits,
-//     x ~= e * (q1 + q2 / 256) = e * T / 256 with e the smallest power of two >= max|x| / 127
-//     and T = rint(256 x / e). The error is at most e / 512 per value (< 3.1e-5 of the block's
-//     largest magnitude), integer activations are exact, and the int32 products of both digits
-//     are exact. S_s is the f32 sum of the unquantized values.
+//   * activation operand: every 32-value sub-block of a token is quantized to three int8
+//     digits, x ~= e * (q1 + q2 / 256 + q3 / 65536) = e * T / 65536 with e the smallest power of
+//     two >= max|x| / 63 and T = rint(65536 x / e). The error is at most e / 2^17 per value
+//     (< 2.4e-7 of the block's largest magnitude, so a lone huge value leaves its block-mates
+//     ~22 bits), integer activations below 2^22 are exact, and the int32 products of every
+//     digit are exact. S_s is the f32 sum of the unquantized values.
 //
 // Accumulator layout. One MFMA covers one 32-byte chunk c of a row's nibbles (sub-block 2c in
-// the low nibbles, 2c + 1 in the high nibbles) for the 16 rows of a tile. Its 16 operand rows
-// stand for (sub-block, token, digit) triples, so the four chunks of a super-block accumulate
-// into the SAME result: each lane loads its activation digits only into the operand of the MFMA
-// whose sub-block owns the lane's row (an exec-masked LDS read) and the other operands keep
-// zeros in that lane. For one token the 16 rows are the 8 sub-blocks x 2 digits, every result
-// lane is useful, and result lane group g holds sub-blocks g and g + 4 of the 16 output rows.
-// Two tokens use two results (sub-blocks 0-3, 4-7), four tokens one result per chunk.
+// the low nibbles, 2c + 1 in the high nibbles) for the 16 rows of a tile. A result's 16 operand
+// rows are four groups of four: group g stands for one (sub-block, token) and its rows for the
+// three digits and a zero row. Result lane group g then holds exactly that group's three digit
+// sums for the 16 output rows (D[0..2]; D[3] is zero).
+//   * one token: two results, sub-blocks 0-3 and 4-7 (chunks 0-1 and 2-3 each accumulate into
+//     one result); a lane loads activation digits for the two chunks its group belongs to;
+//   * two tokens: one result per chunk, groups (parity of the sub-block, token);
+//   * three or four tokens: one result per sub-block (two per chunk), groups = tokens.
+// Operand rows whose sub-block parity varies across the lanes of one result read their 16 bytes
+// from a "split" unit (P0 | 8 zero bytes | P1) at offset 0 or 8, so every lane's operand is
+// {its digits, zeros} in the right half without a per-lane select.
 //
 // Work split: a workgroup owns TW 16-row tiles, each worked by KW waves on contiguous parts of
 // the super-blocks. The workgroup quantizes the activations of all of K once into LDS for its
@@ -52,44 +57,67 @@ namespace {
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 // ---- Activation operand layout for MP (1, 2, 4) token rows --------------------------------
-// Per super-block: MP result blocks of 16 rows x 4 lane groups x 16 bytes (entry index
-// ((bl * MP + blk) * 16 + row) * 4 + g), then per (sub-block, token) a float2 {e, S}.
-// Row `row` of block `blk` holds digit k of token t for sub-block sig (positions 8g..8g+7 of
-// the sub-block in bytes 0-7 when sig is even, bytes 8-15 when odd; the other half is zero).
+// Per super-block slot: the A units, then the {e, S} pairs.
+// A unit (chunk c, token t, digit k, lane group g) holds the digit-k bytes of values 8g..8g+7 of
+// sub-blocks 2c (payload P0) and 2c + 1 (P1) of token t: for one and two tokens 24 bytes
+// P0 | 0 x 8 | P1 (a 16-byte read at offset 0 gives {P0, 0}, at offset 8 {0, P1}); for four
+// tokens 16 bytes P0 | P1 (both halves feed the two MFMAs of the chunk).
 template <int MP>
-__host__ __device__ constexpr int blk_of(int sig) {
-  return MP == 1 ? 0 : MP == 2 ? sig >> 2 : sig >> 1;
+__host__ __device__ constexpr int unit_bytes() { return MP == 4 ? 16 : 24; }
+template <int MP>
+__host__ __device__ constexpr int unit_of(int c, int t, int k, int g) {
+  return ((c * MP + t) * 3 + k) * 4 + g;
 }
 template <int MP>
-__host__ __device__ constexpr int row_of(int sig, int t, int k) {
-  return MP == 1 ? 4 * (sig & 3) + 2 * (sig >> 2) + k
-       : MP == 2 ? 4 * (sig & 3) + 2 * t + k
-                 : 8 * (sig & 1) + 2 * t + k;
-}
-// Inverse: result block `blk`, lane group gq, pair p (result elements 2p, 2p + 1 = digits 0, 1)
-// hold sub-block 4 * sig_hi + sig_q and token tok_of.
+__host__ __device__ constexpr size_t a_bytes() { return (size_t)48 * MP * unit_bytes<MP>(); }
+// Byte offset of the payload of sub-block sig (token t, digit k, lane group g) in a slot.
 template <int MP>
-__host__ __device__ constexpr bool sig_hi(int blk, int p) {
-  return MP == 1 ? p == 1 : MP == 2 ? blk == 1 : blk >= 2;
+__host__ __device__ constexpr size_t pay_off(int sig, int t, int k, int g) {
+  return (size_t)unit_of<MP>(sig >> 1, t, k, g) * unit_bytes<MP>() +
+         (size_t)(sig & 1) * (MP == 4 ? 8 : 16);
+}
+// Results per record, and the result lane group g's (sub-block, token) in result rho.
+template <int MP>
+__host__ __device__ constexpr int n_res() { return 2 * MP; }
+template <int MP>
+__host__ __device__ constexpr int res_sig(int rho, int g) {
+  return MP == 1 ? 4 * rho + g : MP == 2 ? 2 * rho + (g >> 1) : rho;
 }
 template <int MP>
-__host__ __device__ constexpr int sig_q(int blk, int gq) {
-  return MP == 4 ? 2 * (blk & 1) + (gq >> 1) : gq;
+__host__ __device__ constexpr bool res_hi(int rho) {  // res_sig >= 4
+  return MP == 1 ? rho == 1 : MP == 2 ? rho >= 2 : rho >= 4;
 }
 template <int MP>
-__host__ __device__ constexpr int tok_of(int gq, int p) {
-  return MP == 1 ? 0 : MP == 2 ? p : 2 * (gq & 1) + p;
+__host__ __device__ constexpr int lane_tok(int g) {
+  return MP == 1 ? 0 : MP == 2 ? (g & 1) : g;
 }
-// Index of the {e, S} pair of (sub-block, token); the two pairs a lane reads for one result
-// block are adjacent, the first at an even index.
+// Index of the {e, S} pair of (sub-block, token): result rho of lane group g reads pair
+// 2 * es4_of(rho >> 1, g) + (rho & 1), so a lane's pairs come two to a float4.
+template <int MP>
+__host__ __device__ constexpr int es4_of(int j, int g) {
+  return MP == 1 ? g : MP == 2 ? (j * 2 + (g >> 1)) * 2 + (g & 1) : g * 4 + j;
+}
 template <int MP>
 __host__ __device__ constexpr int es_of(int sig, int t) {
-  return MP == 1 ? 2 * (sig & 3) + (sig >> 2) : sig * MP + t;
+  return MP == 1 ? 2 * (sig & 3) + (sig >> 2)
+       : MP == 2 ? 2 * ((((sig >> 2) * 2 + (sig & 1)) * 2) + t) + ((sig >> 1) & 1)
+                 : 8 * t + sig;
 }
 // Bytes of the operands of one super-block.
 template <int MP>
-__host__ __device__ constexpr size_t op_bytes() { return (size_t)MP * 1024 + (size_t)MP * 64; }
+__host__ __device__ constexpr size_t op_bytes() { return a_bytes<MP>() + (size_t)MP * 64; }
 
+// The block scale of a sub-block whose largest magnitude has bit pattern mb: e = 2^k, the
+// smallest power of two with 63 e >= amax (amax = f 2^E, f in [0.5, 1)), so |x| / e <= 63 and
+// x / e is exact. Non-finite blocks get e = NaN, which carries into every output that uses them.
+__device__ __forceinline__ float block_scale(float amax, int &k) {
+  int E;
+  const float f = frexpf(amax, &E);
+  k = E - 6 + (f > 63.f / 64.f ? 1 : 0);
+  float e = amax > 0.f ? ldexpf(1.f, k) : 0.f;
+  if (!(amax <= 3.4e38f)) e = __builtin_nanf("");
+  return e;
+}
 
 // The 32 values of one sub-block of one token (zeros when !valid).
 __device__ __forceinline__ void load_block(const float *__restrict__ x, bool valid, float (&v)[32]) {
@@ -118,49 +146,40 @@ __device__ __forceinline__ float block_sum(const float (&v)[32]) {
   return quad_sum(p[0], p[1], p[2], p[3]) + quad_sum(p[4], p[5], p[6], p[7]);
 }
 
-// Quantize the 32 values v of sub-block sig of token t into the layout above.
-// A: operand entries of super-block slot bl; ES: its {e, S} pairs.
+// Quantize the 32 values v of sub-block sig of token t into a slot: A the slot's operand bytes,
+// ES its {e, S} pairs.
 template <int MP>
 __device__ __forceinline__ void quant_vals(const float (&v)[32], int sig, int t,
-                                           uint4 *__restrict__ A, float2 *__restrict__ ES) {
+                                           unsigned char *__restrict__ A, float2 *__restrict__ ES) {
   uint32_t mb = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     mb = max(mb, absmax4_bits(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]));
-  const float amax = __uint_as_float(mb);  // a NaN when the block holds one
-  const float s = block_sum(v);
-  // e = 2^k, the smallest power of two with 127 e >= amax (amax = f 2^E, f in [0.5, 1)), so
-  // x / e is exact and integer activations quantize without error. Non-finite blocks get
-  // e = NaN, which carries into every output that uses them.
-  int E;
-  const float f = frexpf(amax, &E);
-  const int k = E - 7 + (f > 127.f / 128.f ? 1 : 0);
-  float e = amax > 0.f ? ldexpf(1.f, k) : 0.f;
-  if (!(amax <= 3.4e38f)) e = __builtin_nanf("");
-  ES[es_of<MP>(sig, t)] = make_float2(e, s);
-
-  // T = rint(256 x / e), |T| <= 32512, so x ~= e T / 256 to within e / 512. The digits are
-  // q1 = (T + 128) >> 8 (byte 1 of T + 128) and q2 = T - 256 q1 in [-128, 127] (the low byte
-  // of T), as two's complement bytes: q1 + q2 / 256 = T / 256 exactly (digits4). Each lane
-  // group's eight values are written as soon as they are packed.
-  const int sh = 8 - k;
-  const int blk = blk_of<MP>(sig);
-  uint4 *row0 = A + ((size_t)blk * 16 + row_of<MP>(sig, t, 0)) * 4;
-  uint4 *row1 = A + ((size_t)blk * 16 + row_of<MP>(sig, t, 1)) * 4;
+  int k;
+  const float e = block_scale(__uint_as_float(mb), k);  // a NaN when the block holds one
+  ES[es_of<MP>(sig, t)] = make_float2(e, block_sum(v));
+  // T = rint(65536 x / e), |T| <= 63 * 65536: digits3.
+  const int sh = 16 - k;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    uint32_t a0, a1, c0, c1;
-    digits4(v[8 * g], v[8 * g + 1], v[8 * g + 2], v[8 * g + 3], sh, a0, c0);
-    digits4(v[8 * g + 4], v[8 * g + 5], v[8 * g + 6], v[8 * g + 7], sh, a1, c1);
-    row0[g] = (sig & 1) ? make_uint4(0, 0, a0, a1) : make_uint4(a0, a1, 0, 0);
-    row1[g] = (sig & 1) ? make_uint4(0, 0, c0, c1) : make_uint4(c0, c1, 0, 0);
+    uint32_t a0, b0, c0, a1, b1, c1;
+    digits3(v[8 * g], v[8 * g + 1], v[8 * g + 2], v[8 * g + 3], sh, a0, b0, c0);
+    digits3(v[8 * g + 4], v[8 * g + 5], v[8 * g + 6], v[8 * g + 7], sh, a1, b1, c1);
+    *reinterpret_cast<uint2 *>(A + pay_off<MP>(sig, t, 0, g)) = make_uint2(a0, a1);
+    *reinterpret_cast<uint2 *>(A + pay_off<MP>(sig, t, 1, g)) = make_uint2(b0, b1);
+    *reinterpret_cast<uint2 *>(A + pay_off<MP>(sig, t, 2, g)) = make_uint2(c0, c1);
+    if (MP != 4 && !(sig & 1))
+#pragma unroll
+      for (int d = 0; d < 3; ++d)
+        *reinterpret_cast<uint2 *>(A + (size_t)unit_of<MP>(sig >> 1, t, d, g) * 24 + 8) =
+            make_uint2(0u, 0u);
   }
 }
 
-// Quantize one 32-value sub-block of one token (zeros when !valid) into the layout above.
+// Quantize one 32-value sub-block of one token (zeros when !valid) into a slot.
 template <int MP>
 __device__ __forceinline__ void quant_block(const float *__restrict__ x, bool valid, int sig,
-                                            int t, uint4 *__restrict__ A,
+                                            int t, unsigned char *__restrict__ A,
                                             float2 *__restrict__ ES) {
   float v[32];
   load_block(x, valid, v);
@@ -179,56 +198,56 @@ __device__ __forceinline__ void quant_block(const float *__restrict__ x, bool va
 
 // The block maximum is taken on magnitude bit patterns (absmax4_bits): one DPP max per step, where
 // fmaxf needed a NaN-quieting max and a separate DPP move. The digits use one fma per value
-// (digits4s) unless a lane's scale 2^(8 - k) is not a normal float (blocks below ~2^-120, where
+// (digits3s) unless a lane's scale 2^(16 - k) is not a normal float (blocks below ~2^-105, where
 // the wave takes ldexpf).
 template <int MP>
 __device__ __forceinline__ void quant_lanes(const float4 v, int lane, int t,
-                                            uint4 *__restrict__ A, float2 *__restrict__ ES) {
+                                            unsigned char *__restrict__ A,
+                                            float2 *__restrict__ ES) {
   const int sig = lane >> 3, p = lane & 7;
   uint32_t mb = absmax4_bits(v.x, v.y, v.z, v.w);
   mb = max(mb, FHIP_DPP_U(mb, 0xB1));   // quad_perm [1,0,3,2]: lane ^ 1
   mb = max(mb, FHIP_DPP_U(mb, 0x4E));   // quad_perm [2,3,0,1]: lane ^ 2
   mb = max(mb, FHIP_DPP_U(mb, 0x141));  // row_half_mirror: the other quad of the eight
-  const float amax = __uint_as_float(mb);  // a NaN when the block holds one
   float sum = quad_sum(v.x, v.y, v.z, v.w);
   sum = sum + FHIP_DPP(sum, 0xB1);
   sum = sum + FHIP_DPP(sum, 0x4E);
   sum = sum + FHIP_DPP(sum, 0x141);
-  int E;
-  const float f = frexpf(amax, &E);
-  const int k = E - 7 + (f > 127.f / 128.f ? 1 : 0);
-  float e = amax > 0.f ? ldexpf(1.f, k) : 0.f;
-  if (!(amax <= 3.4e38f)) e = __builtin_nanf("");
+  int k;
+  const float e = block_scale(__uint_as_float(mb), k);  // a NaN when the block holds one
   if (p == 0) ES[es_of<MP>(sig, t)] = make_float2(e, sum);
-  uint32_t a, c;
-  const int sh = 8 - k;
+  uint32_t a, b, c;
+  const int sh = 16 - k;
   if (__builtin_expect(__builtin_amdgcn_ballot_w64(sh > 127) == 0, 1))
-    digits4s(v.x, v.y, v.z, v.w, ldexpf(1.f, sh), a, c);
+    digits3s(v.x, v.y, v.z, v.w, ldexpf(1.f, sh), a, b, c);
   else
-    digits4(v.x, v.y, v.z, v.w, sh, a, c);
-  const int blk = blk_of<MP>(sig), g = p >> 1, half = p & 1;
-  uint32_t *row0 = reinterpret_cast<uint32_t *>(A + ((size_t)blk * 16 + row_of<MP>(sig, t, 0)) * 4 + g);
-  uint32_t *row1 = reinterpret_cast<uint32_t *>(A + ((size_t)blk * 16 + row_of<MP>(sig, t, 1)) * 4 + g);
-  const int dw = 2 * (sig & 1) + half, dz = 2 * ((sig & 1) ^ 1) + half;
-  row0[dw] = a;
-  row0[dz] = 0u;
-  row1[dw] = c;
-  row1[dz] = 0u;
+    digits3(v.x, v.y, v.z, v.w, sh, a, b, c);
+  const int g = p >> 1, h = 4 * (p & 1);
+  const uint32_t dig[3] = {a, b, c};
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    uint32_t *u = reinterpret_cast<uint32_t *>(A + (size_t)unit_of<MP>(sig >> 1, t, d, g) *
+                                                       unit_bytes<MP>() + h);
+    u[(sig & 1) * (MP == 4 ? 2 : 4)] = dig[d];
+    // Split units: both sub-blocks' lanes write the zero dword between the payloads (the same
+    // value twice), so no lane branches.
+    if (MP != 4) u[2] = 0u;
+  }
 }
 
 // Quantize super-blocks [s0, s0 + nb) of M tokens (tokens M..MP-1 zero) into slots 0..nb-1 of
 // the operand buffers, `lane` of `nlanes` threads sharing the work.
 template <int MP>
 __device__ __forceinline__ void quant_range(const float *__restrict__ X, int K, int M, int s0,
-                                            int nb, uint4 *__restrict__ A, float2 *__restrict__ ES,
-                                            int lane, int nlanes) {
+                                            int nb, unsigned char *__restrict__ A,
+                                            float2 *__restrict__ ES, int lane, int nlanes) {
   const int per_t = nb * 8;
   for (int task = lane; task < per_t * MP; task += nlanes) {
     const int t = task / per_t, rest = task - t * per_t;
     const int bl = rest >> 3, sig = rest & 7;
     const bool valid = t < M;
     quant_block<MP>(X + (valid ? (size_t)t * K + 256 * (size_t)(s0 + bl) + 32 * sig : 0), valid,
-                    sig, t, A + (size_t)bl * MP * 64, ES + (size_t)bl * 8 * MP);
+                    sig, t, A + (size_t)bl * a_bytes<MP>(), ES + (size_t)bl * 8 * MP);
   }
 }
 
@@ -249,11 +268,40 @@ __device__ __forceinline__ void scale_min(uint32_t y, uint32_t z, uint32_t w, bo
   mn = (float)m;
 }
 
+// The eight 6-bit scales and mins of a row header (GetScaleMinK4 for j = 0..7), byte-parallel:
+// byte i of sc[0] / mn[0] is the scale / min of sub-block i, of sc[1] / mn[1] sub-block 4 + i.
+__device__ __forceinline__ void scale_min8(uint32_t y, uint32_t z, uint32_t w, uint32_t (&sc)[2],
+                                           uint32_t (&mn)[2]) {
+  const uint32_t m6 = 0x3F3F3F3Fu, m4 = 0x0F0F0F0Fu, m2 = 0x30303030u;
+  sc[0] = y & m6;
+  mn[0] = z & m6;
+  sc[1] = (w & m4) | ((y >> 2) & m2);
+  mn[1] = ((w >> 4) & m4) | ((z >> 2) & m2);
+}
+// Byte i of v as a float (one v_cvt_f32_ubyte<i>).
+__device__ __forceinline__ float ubyte_f32(uint32_t v, int i) {
+  return (float)((v >> (8 * i)) & 0xFFu);
+}
+
+// 65536 d0 + 256 d1 + d2 as two shift-adds. The empty asm (no instruction) only stops the
+// compiler from re-associating the sum into three instructions; the arithmetic itself stays
+// compiler code, which knows to wait for the MFMA results it reads.
+__device__ __forceinline__ int digit_sum(int d0, int d1, int d2) {
+  int t = (d0 << 8) + d1;
+  asm volatile("" : "+v"(t));
+  return (t << 8) + d2;
+}
+
 // silu(z) = z / (1 + e^-z) with e^-z evaluated in double and rounded to f32, the operation
 // order of internal/model/forward.go:452.
 __device__ __forceinline__ float silu_f32(float z) {
   return z / (1.f + (float)exp(-(double)z));
 }
+
+// Weight records each wave keeps in flight (LDS path) and the widest workgroup (waves) for one
+// token. Measured at the 7B FFN shapes: an 8-record ring with 8-wave workgroups, the
+// activation loads issued ahead of the ring, and lane-parallel coalesced quantization were all
+// slower (11.9-12 us gate/up, 14.7-15.1 us down, against 10.6 and 13.8 us here).
 
 // Weight records each wave keeps in flight (LDS path) and the widest workgroup (waves) for one
 // token. Measured at the 7B FFN shapes: an 8-record ring with 8-wave workgroups, the
@@ -274,9 +322,9 @@ constexpr int kXPre = 8;
 enum { kXLate = 0, kXSpread = 1, kXOwn = 2 };
 template <int MP, bool LX, bool SWIGLU, int XM, int PF0, bool EX>
 __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_kernel(
-    const GemvGroup grp, const float *__restrict__ X, const uint4 *__restrict__ xg, int K, int M,
-    int nblk, int TW, int KW) {
-  constexpr int NT = MP == 1 ? 1 : 2;  // token slots per lane
+    const GemvGroup grp, const float *__restrict__ X, const unsigned char *__restrict__ xg, int K,
+    int M, int nblk, int TW, int KW) {
+  constexpr int NR = n_res<MP>();
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: SGPRs
@@ -348,26 +396,28 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
 
   // Operands: in LDS, quantized once by the whole workgroup for its TW tiles, or the prepared
   // global buffer; slot = super-block either way.
-  const unsigned char *opb = LX ? smem : reinterpret_cast<const unsigned char *>(xg);
-  const uint4 *A = reinterpret_cast<const uint4 *>(opb);
-  const float2 *ES = reinterpret_cast<const float2 *>(opb + (size_t)nblk * MP * 1024);
+  const unsigned char *opA = LX ? smem : xg;
+  const float4 *ES4 = reinterpret_cast<const float4 *>(opA + (size_t)nblk * a_bytes<MP>());
   float *red = reinterpret_cast<float *>(smem + (LX ? (size_t)nblk * op_bytes<MP>() : 0));
 
-  // A lane's operand row belongs to one chunk per result block; with one or two tokens the
-  // lane loads only for the MFMA of that chunk.
-  auto lane_chunk = [&](int blk) {
-    const int p = (r >> 1) & 1;
-    const int sig = 4 * (sig_hi<MP>(blk, p) ? 1 : 0) + sig_q<MP>(blk, r >> 2);
-    return sig >> 1;
+  // This lane's operand row: group ag = r >> 2 of its results, digit ad = r & 3 (3: the zero
+  // row). With one token the group is sub-block 4 rho + ag, in chunks (ag >> 1) and
+  // 2 + (ag >> 1); with two tokens (parity ag >> 1, token ag & 1) of every chunk; with four
+  // tokens token ag of every chunk (both halves of the unit: the chunk's two results).
+  const int ag = r >> 2, ad = r & 3;
+  const bool arow = ad < 3;
+  const int adc = arow ? ad : 2;  // a valid unit for the zero rows' (unused) global loads
+  auto a_off = [&](int c) -> size_t {
+    if (MP == 1) return (size_t)unit_of<1>(c, 0, adc, gq) * 24 + 8 * (ag & 1);
+    if (MP == 2) return (size_t)unit_of<2>(c, ag & 1, adc, gq) * 24 + 8 * (ag >> 1);
+    return (size_t)unit_of<4>(c, ag, adc, gq) * 16;
   };
-  auto a_index = [&](int slot, int m) {  // this lane's entry for the MFMA of chunk m
-    const int blk = m * MP / 4;
-    return ((size_t)(slot * MP + blk) * 16 + r) * 4 + gq;
-  };
-  auto es_index = [&](int slot, int blk) {  // float4 holding this lane's two {e, S} pairs
-    return ((size_t)slot * 8 * MP +
-            es_of<MP>(4 * (sig_hi<MP>(blk, 0) ? 1 : 0) + sig_q<MP>(blk, gq), tok_of<MP>(gq, 0))) /
-           2;
+  auto a_own = [&](int c) { return arow && (MP != 1 || (c & 1) == (ag >> 1)); };
+  const unsigned char *alane = opA + a_off(0);  // LDS path: this lane's operand in slot 0
+  auto ld16 = [](const unsigned char *p) {  // 8-byte aligned
+    const uint2 lo = *reinterpret_cast<const uint2 *>(p);
+    const uint2 hi = *reinterpret_cast<const uint2 *>(p + 8);
+    return i32x4{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
   };
 
   struct Ops {
@@ -383,24 +433,25 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
     if (!LX) {
       // Every lane loads all four (an exec-masked load made the compiler wait for the whole
       // ring after it); the lanes that do not own a chunk zero it at use.
+      const unsigned char *slot = opA + (size_t)b * a_bytes<MP>();
 #pragma unroll
-      for (int m = 0; m < 4; ++m) o.a[m] = __builtin_bit_cast(i32x4, A[a_index(b, m)]);
+      for (int c = 0; c < 4; ++c) o.a[c] = ld16(slot + a_off(c));
 #pragma unroll
-      for (int blk = 0; blk < MP; ++blk)
-        o.es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b, blk)];
+      for (int j = 0; j < MP; ++j) o.es[j] = ES4[(size_t)b * 4 * MP + es4_of<MP>(j, gq)];
     }
   };
-
   constexpr int PF = LX ? (MP == 1 ? kPF1 : 4) : 2;
   Ops ring[PF];
 #pragma unroll
   for (int u = 0; u < PF; ++u) {
     if (!LX)
 #pragma unroll
-      for (int m = 0; m < 4; ++m) ring[u].a[m] = i32x4{0, 0, 0, 0};
+      for (int c = 0; c < 4; ++c) ring[u].a[c] = i32x4{0, 0, 0, 0};
     if (!xpre || u < PF0) load(min(b0 + u, b1 - 1), ring[u]);  // a repeat is never used
   }
   // With the first records in flight, the workgroup quantizes the activations of its K range.
+  unsigned char *wA = const_cast<unsigned char *>(opA);
+  float2 *wES = reinterpret_cast<float2 *>(const_cast<float4 *>(ES4));
   if (LX) {
     if (xown) {
       // Only this wave reads these slots: LDS accesses of one wave complete in order, so no
@@ -412,8 +463,8 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
         for (int i = 0; i < kPT; ++i)
           if (i < onb)
             quant_lanes<MP>(MP == 1 || t < M ? xv[t * kPT + i] : z, lane, t,
-                            const_cast<uint4 *>(A) + (size_t)(ob0 + i) * MP * 64,
-                            const_cast<float2 *>(ES) + (size_t)(ob0 + i) * 8 * MP);
+                            wA + (size_t)(ob0 + i) * a_bytes<MP>(),
+                            wES + (size_t)(ob0 + i) * 8 * MP);
     } else if (xpre) {
 #pragma unroll
       for (int j = 0; j < kXPre; ++j) {
@@ -421,13 +472,12 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
         if (c < nchunk) {
           const int t = chunk_tok(c), bl = c - t * nblk;
           const float4 z = {0.f, 0.f, 0.f, 0.f};
-          quant_lanes<MP>(MP == 1 || t < M ? xv[j] : z, lane, t, const_cast<uint4 *>(A) + (size_t)bl * MP * 64,
-                          const_cast<float2 *>(ES) + (size_t)bl * 8 * MP);
+          quant_lanes<MP>(MP == 1 || t < M ? xv[j] : z, lane, t, wA + (size_t)bl * a_bytes<MP>(),
+                          wES + (size_t)bl * 8 * MP);
         }
       }
     } else {
-      quant_range<MP>(X, K, M, 0, nblk, const_cast<uint4 *>(A), const_cast<float2 *>(ES),
-                      threadIdx.x, blockDim.x);
+      quant_range<MP>(X, K, M, 0, nblk, wA, wES, threadIdx.x, blockDim.x);
     }
     if (!xown) __syncthreads();
     if (xpre)
@@ -436,15 +486,14 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
   }
   const uint32_t k0F = 0x0F0F0F0Fu;
 
-  // LDS path: the activation operands of the current super-block. Lanes that a given MFMA does
-  // not load for keep zeros there for the whole kernel.
-  i32x4 areg[4];
+  // The activation operands of the current super-block, one per chunk; with four tokens the
+  // chunk's unit is split into its two MFMA operands, each with a zero half that is never
+  // written. Operands a lane does not load stay zero in that lane for the whole kernel.
+  i32x4 areg[4], alo[4], ahi[4];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) areg[m] = i32x4{0, 0, 0, 0};
+  for (int c = 0; c < 4; ++c) areg[c] = alo[c] = ahi[c] = i32x4{0, 0, 0, 0};
 
-  float acc[NT];
-#pragma unroll
-  for (int s = 0; s < NT; ++s) acc[s] = 0.f;
+  float acc = 0.f;
 
   for (int bb = b0; bb < b1; bb += PF) {
 #pragma unroll
@@ -454,129 +503,171 @@ __global__ __launch_bounds__(MP == 1 ? 64 * kMaxWaves1 : 512) void q4k_gemv_i8_k
       // This slot's three loads are older than the other slots' refills: saying so lets the
       // compiler wait for just this record instead of draining the ring at the top of a pass.
       if (LX) __builtin_amdgcn_s_waitcnt(0x0F70 | (3 * (PF - 1)));
-      else __builtin_amdgcn_s_waitcnt(0x0F70 | ((7 + MP) * (PF - 1)));  // < 16 loads: PF = 2
+      else __builtin_amdgcn_s_waitcnt(0x0F70 | ((11 + MP) * (PF - 1)));  // 3 + 8 + MP loads: < 16
       Ops &cur = ring[u];
 
       float4 es[MP];
       if (LX) {
+        // The slot's base is a scalar: one address add per record, and each chunk's offset
+        // (a_off(c) - a_off(0), a constant) fits the LDS instructions' immediate fields.
+        const unsigned char *slot =
+            alane + __builtin_amdgcn_readfirstlane((int)((size_t)b * a_bytes<MP>()));
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          if (MP == 4 || lane_chunk(m * MP / 4) == m)
-            areg[m] = __builtin_bit_cast(i32x4, A[a_index(b, m)]);
+        for (int c = 0; c < 4; ++c) {
+          if (!a_own(c)) continue;
+          constexpr int kCS = a_bytes<MP>() / 4;  // a_off(c) = a_off(0) + c * kCS
+          const uint2 lo = *reinterpret_cast<const uint2 *>(slot + c * kCS);
+          const uint2 hi = *reinterpret_cast<const uint2 *>(slot + c * kCS + 8);
+          if (MP == 4) {
+            alo[c][0] = (int)lo.x; alo[c][1] = (int)lo.y;
+            ahi[c][2] = (int)hi.x; ahi[c][3] = (int)hi.y;
+          } else {
+            areg[c] = i32x4{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+          }
+        }
+        const float4 *es4 =
+            ES4 + __builtin_amdgcn_readfirstlane((int)((size_t)b * 4 * MP));
 #pragma unroll
-        for (int blk = 0; blk < MP; ++blk)
-          es[blk] = reinterpret_cast<const float4 *>(ES)[es_index(b, blk)];
+        for (int j = 0; j < MP; ++j) es[j] = es4[es4_of<MP>(j, gq)];
       } else {
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          areg[m] = MP == 4 || lane_chunk(m * MP / 4) == m ? cur.a[m] : i32x4{0, 0, 0, 0};
+        for (int c = 0; c < 4; ++c) {
+          const i32x4 v = a_own(c) ? cur.a[c] : i32x4{0, 0, 0, 0};
+          if (MP == 4) {
+            alo[c][0] = v[0]; alo[c][1] = v[1];
+            ahi[c][2] = v[2]; ahi[c][3] = v[3];
+          } else {
+            areg[c] = v;
+          }
+        }
 #pragma unroll
-        for (int blk = 0; blk < MP; ++blk) es[blk] = cur.es[blk];
+        for (int j = 0; j < MP; ++j) es[j] = cur.es[j];
       }
 
       // Weight operands: chunk c = words 2c, 2c+1 of the lane's 32 bytes (8 nibble positions
       // of the chunk), low nibbles -> slots 0-7 (sub-block 2c), high -> slots 8-15 (2c + 1).
       const uint32_t q[8] = {cur.qa.x, cur.qa.y, cur.qa.z, cur.qa.w,
                              cur.qb.x, cur.qb.y, cur.qb.z, cur.qb.w};
-      i32x4 D[MP];
+      i32x4 D[NR];
 #pragma unroll
-      for (int blk = 0; blk < MP; ++blk) D[blk] = i32x4{0, 0, 0, 0};
+      for (int rho = 0; rho < NR; ++rho) D[rho] = i32x4{0, 0, 0, 0};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const i32x4 B = {(int)(q[2 * c] & k0F), (int)(q[2 * c + 1] & k0F),
                          (int)((q[2 * c] >> 4) & k0F), (int)((q[2 * c + 1] >> 4) & k0F)};
-        const int blk = c * MP / 4;
-        D[blk] = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[c], B, D[blk], 0, 0, 0);
+        if (MP == 4) {
+          D[2 * c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[c], B, D[2 * c], 0, 0, 0);
+          D[2 * c + 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[c], B, D[2 * c + 1], 0, 0, 0);
+        } else {
+          const int rho = MP == 1 ? c >> 1 : c;
+          D[rho] = __builtin_amdgcn_mfma_i32_16x16x64_i8(areg[c], B, D[rho], 0, 0, 0);
+        }
       }
-      // The slot is refilled with the record PF ahead as soon as its operands are consumed;
-      // the header words are kept for the scaling below.
+      // The header is decoded into what the epilogue needs (d, dmin and the scales and mins;
+      // two and four tokens: every sub-block's, byte-parallel, with two tokens lane group g's
+      // sub-blocks 2 rho + (g >> 1) brought to bytes 0 and 2 of each word), so that the slot
+      // can be refilled right after: nothing then reads the old header behind the new load.
       const uint4 h = cur.h;
+      float dd = (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xffffu));
+      float dmn = (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16));
+      uint32_t sc8[2], mn8[2];
+      float sc1[NR], mn1[NR];
+      if (MP >= 2) {
+        scale_min8(h.y, h.z, h.w, sc8, mn8);
+        if (MP == 2) {
+          const uint32_t sh = 8u * (uint32_t)(gq >> 1);
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            sc8[i] >>= sh;
+            mn8[i] >>= sh;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int rho = 0; rho < NR; ++rho)
+          scale_min(h.y, h.z, h.w, res_hi<MP>(rho), res_sig<MP>(rho, gq) & 3, sc1[rho], mn1[rho]);
+      }
+      // The slot is refilled with the record PF ahead once its operands and header are
+      // consumed. The empty asm pins the decoded values before the refill's branch (otherwise
+      // the decode sinks below it), and nothing moves across the barrier: either way the
+      // header would need a second register and a copy back that waits for the new load.
+      asm volatile("" : "+v"(dd), "+v"(dmn));
+#pragma unroll
+      for (int i = 0; i < (MP >= 2 ? 2 : 0); ++i) asm volatile("" : "+v"(sc8[i]), "+v"(mn8[i]));
+#pragma unroll
+      for (int rho = 0; rho < (MP == 1 ? NR : 0); ++rho)
+        asm volatile("" : "+v"(sc1[rho]), "+v"(mn1[rho]));
+      __builtin_amdgcn_sched_barrier(0);
       if (EX)
         load(min(b + PF, b1 - 1), cur);
       else if (b + PF < b1)
         load(b + PF, cur);
 
-      const float dd = (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xffffu));
-      const float dmn = (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16));
-      float xs[NT], vs[NT];
+      // Per result: T-sum = 65536 D0 + 256 D1 + D2 (exact in int32: |D0| <= 32 * 15 * 63), then
+      // sc * e * T-sum; the 2^-16 of the digits is folded into d.
+      float xs = 0.f, vs = 0.f;
 #pragma unroll
-      for (int s = 0; s < NT; ++s) xs[s] = vs[s] = 0.f;
-#pragma unroll
-      for (int blk = 0; blk < MP; ++blk)
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          float sc, mn;
-          scale_min(h.y, h.z, h.w, sig_hi<MP>(blk, p), sig_q<MP>(blk, gq), sc, mn);
-          const float val = fmaf((float)D[blk][2 * p + 1], 1.f / 256.f, (float)D[blk][2 * p]);
-          const float e = p ? es[blk].z : es[blk].x;
-          const float S = p ? es[blk].w : es[blk].y;
-          const int s = MP == 1 ? 0 : p;
-          xs[s] = fmaf(sc, e * val, xs[s]);
-          vs[s] = fmaf(mn, S, vs[s]);
+      for (int rho = 0; rho < NR; ++rho) {
+        float sc, mn;
+        if (MP >= 2) {
+          const int byte = MP == 4 ? rho & 3 : 2 * (rho & 1);  // sub-block rho, or 2 rho + (g >> 1)
+          sc = ubyte_f32(sc8[rho >> (MP == 4 ? 2 : 1)], byte);
+          mn = ubyte_f32(mn8[rho >> (MP == 4 ? 2 : 1)], byte);
+        } else {
+          sc = sc1[rho];
+          mn = mn1[rho];
         }
-#pragma unroll
-      for (int s = 0; s < NT; ++s) acc[s] = fmaf(dd, xs[s], fmaf(-dmn, vs[s], acc[s]));
+        const int ts = digit_sum(D[rho][0], D[rho][1], D[rho][2]);
+        const float4 ep = es[rho >> 1];
+        const float e = (rho & 1) ? ep.z : ep.x;
+        const float S = (rho & 1) ? ep.w : ep.y;
+        xs = fmaf(sc, e * (float)ts, xs);
+        vs = fmaf(mn, S, vs);
+      }
+      acc = fmaf(dd * (1.f / 65536.f), xs, fmaf(-dmn, vs, acc));
     }
   }
 
   // Partials of the KW parts go through LDS; part 0 sums them in part order (deterministic),
-  // then adds the lane groups that hold the same (token, row): all four (one or two tokens)
-  // or g and g ^ 2 (four tokens).
-#pragma unroll
-  for (int s = 0; s < NT; ++s) red[((tile * KW + part) * NT + s) * 64 + lane] = acc[s];
+  // then adds the lane groups that hold the same (token, row): all four (one token), g and
+  // g ^ 2 (two tokens); with four tokens lane group g holds token g alone.
+  red[(tile * KW + part) * 64 + lane] = acc;
   __syncthreads();
   const int row = T * 16 + r;
   const bool fin = part == 0 && tvalid;
   if (!SWIGLU && !fin) return;
-  float v[NT];
-#pragma unroll
-  for (int s = 0; s < NT; ++s) {
-    v[s] = acc[s];
-    for (int q = 1; q < KW; ++q) v[s] += red[((tile * KW + q) * NT + s) * 64 + lane];
-    v[s] += __shfl_xor(v[s], 32);
-    if (MP <= 2) v[s] += __shfl_xor(v[s], 16);
-  }
+  float v = acc;
+  for (int q = 1; q < KW; ++q) v += red[(tile * KW + q) * 64 + lane];
+  if (MP <= 2) v += __shfl_xor(v, 32);
+  if (MP == 1) v += __shfl_xor(v, 16);
+  const int t = lane_tok<MP>(gq);
+  const bool writer = gq < MP && t < M;  // lane groups 0..MP-1 hold the tokens
   if (SWIGLU) {
     // Every wave reaches this barrier; the up tile's final values go through LDS to its gate
     // partner (tile + 1 holds up tile T when tile holds gate tile T).
-    float *xch = red + (size_t)blockDim.x / 64 * NT * 64;
-    if (fin)
-#pragma unroll
-      for (int s = 0; s < NT; ++s) xch[(tile * NT + s) * 64 + lane] = v[s];
+    float *xch = red + (size_t)blockDim.x;
+    if (fin) xch[tile * 64 + lane] = v;
     __syncthreads();
     if (!fin || mem != 0) return;
-    if (row < N && gq < (MP == 4 ? 2 : 1)) {
-#pragma unroll
-      for (int s = 0; s < NT; ++s) {
-        const int t = tok_of<MP>(gq, s);
-        if (t < M) Y[(size_t)t * N + row] = silu_f32(v[s]) * xch[((tile + 1) * NT + s) * 64 + lane];
-      }
-    }
+    if (row < N && writer) Y[(size_t)t * N + row] = silu_f32(v) * xch[(tile + 1) * 64 + lane];
     return;
   }
-  if (row < N && gq < (MP == 4 ? 2 : 1)) {
-#pragma unroll
-    for (int s = 0; s < NT; ++s) {
-      const int t = tok_of<MP>(gq, s);
-      if (t < M) Y[(size_t)t * N + row] = v[s];
-    }
-  }
+  if (row < N && writer) Y[(size_t)t * N + row] = v;
 }
 
 // Global-path operand writer: one thread per (token, 32-value sub-block) of all of K.
 template <int MP>
 __global__ void gemv_i8_prep_kernel(const float *__restrict__ X, int K, int M, int nblk,
-                                    uint4 *__restrict__ A) {
+                                    unsigned char *__restrict__ A) {
   const int id = blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= MP * nblk * 8) return;
   const int per_t = nblk * 8;
   const int t = id / per_t, rest = id - t * per_t;
   const int b = rest >> 3, sig = rest & 7;
-  float2 *ES = reinterpret_cast<float2 *>(reinterpret_cast<unsigned char *>(A) +
-                                          (size_t)nblk * MP * 1024);
+  float2 *ES = reinterpret_cast<float2 *>(A + (size_t)nblk * a_bytes<MP>());
   const bool valid = t < M;
   quant_block<MP>(X + (valid ? (size_t)t * K + 256 * (size_t)b + 32 * sig : 0), valid, sig, t,
-                  A + (size_t)b * MP * 64, ES + (size_t)b * 8 * MP);
+                  A + (size_t)b * a_bytes<MP>(), ES + (size_t)b * 8 * MP);
 }
 
 // Workgroup shape: TW tiles x KW waves per tile (TW * KW <= max_waves). Measured on the 7B
@@ -638,12 +729,11 @@ struct I8Plan {
 
 template <int MP>
 I8Plan plan_i8(int ntiles, int K, bool swiglu) {
-  constexpr int NT = MP == 1 ? 1 : 2;
   const int nblk = K / 256;
   const int max_waves = MP == 1 ? kMaxWaves1 : 8;
   I8Plan p{};
   const size_t ldsx = (size_t)nblk * op_bytes<MP>();
-  i8_shape(ntiles, nblk, max_waves, ldsx, (size_t)64 * NT * 4, p.TW, p.KW);
+  i8_shape(ntiles, nblk, max_waves, ldsx, (size_t)64 * 4, p.TW, p.KW);
   // At most two tiles per CU: one workgroup of up to max_waves waves per CU (one tile, or two
   // above one tile per CU), each wave streaming >= 1.5 records (>= 3 for one token on a grid of
   // half the CUs or more, see below). Two to four tokens over 2..8 tiles per CU: eight
@@ -678,7 +768,7 @@ I8Plan plan_i8(int ntiles, int K, bool swiglu) {
     }
   }
   const size_t redB =
-      (size_t)p.TW * p.KW * 64 * NT * 4 + (swiglu ? (size_t)p.TW * 64 * NT * 4 : 0);
+      (size_t)p.TW * p.KW * 64 * 4 + (swiglu ? (size_t)p.TW * 64 * 4 : 0);
   p.lds_x = !tuning().gemv_globalx && ldsx + redB <= (size_t)lds_limit();
   p.lds_bytes = (p.lds_x ? ldsx : 0) + redB;
   p.xop_bytes = p.lds_x ? 0 : (((size_t)nblk * op_bytes<MP>() + 255) & ~(size_t)255);
@@ -697,13 +787,13 @@ int launch_i8(const GemvGroup &g, const float *X, int K, int M, bool swiglu, voi
   if (int rc = check_disjoint("q4k_gemv", X, (size_t)M * K * 4, ws, wsB)) return rc;
   unsigned char *xop = (unsigned char *)ws;
   const int grid = ceil_div(ntiles, p.TW), threads = 64 * p.TW * p.KW;
-  const uint4 *xg = nullptr;
+  const unsigned char *xg = nullptr;
   if (!p.lds_x) {
     const int nprep = MP * nblk * 8;
     gemv_i8_prep_kernel<MP><<<ceil_div(nprep, 128), 128, 0, stream()>>>(X, K, M, nblk,
-                                                                        (uint4 *)xop);
+                                                                        xop);
     FHIP_CHECK_LAUNCH("gemv_i8_prep_kernel");
-    xg = (const uint4 *)xop;
+    xg = xop;
   }
 #define FHIP_I8_LAUNCH_EX(LXV, SWV, XMV, PF0V, EXV)                                          \
   q4k_gemv_i8_kernel<MP, LXV, SWV, XMV, PF0V, EXV><<<grid, threads, p.lds_bytes, stream()>>>( \
