@@ -99,14 +99,24 @@ class HostBuf:
 
 
 class DevBuf:
-    """A device-resident buffer: pointer into the fakhip pool + byte length."""
+    """A device-resident buffer: pointer into the fakhip pool + byte length.
 
-    def __init__(self, ptr: int, nbytes: int):
+    An async op output (a matmul result) records the backend and the fence generation it was
+    enqueued in, and is Ready() only once a host fence (Read) has bumped the generation past it
+    (cudaBuf.Ready, internal/compute/cuda.go:286-300): the stream is FIFO, so one fence
+    materializes every buffer enqueued before it. Synchronous buffers (uploads) have no backend
+    and are ready on return."""
+
+    def __init__(self, ptr: int, nbytes: int, be=None, born_gen: int = 0):
         self.ptr = ptr
         self.nbytes = nbytes
+        self.be = be
+        self.born_gen = born_gen
 
     def Ready(self) -> bool:
-        return True
+        if self.be is None:
+            return True
+        return self.be.fence_gen > self.born_gen
 
 
 @dataclasses.dataclass
@@ -186,6 +196,9 @@ class RocmBackend:
 
     def __init__(self, kq_int8: Optional[bool] = None):
         self.info = fakhip.init()
+        # Host fences (Read) so far; async op outputs are ready once it passes their generation
+        # (cudaBackend.fenceGen, internal/compute/cuda.go:327-331).
+        self.fence_gen = 0
         # upload cache (cuda.go:680-704): (host address, weakref to the owning array, dtype,
         # resident tensor)
         self._upload_cache: list = []
@@ -339,6 +352,9 @@ class RocmBackend:
         out = np.empty(t.Numel(), np.float32)
         if out.size:
             fakhip.call("fhip_d2h", out.ctypes.data, t.buf.ptr, out.size * 4)
+            # The copy drained the stream: everything enqueued before it is materialized
+            # (cuda.go:896).
+            self.fence_gen += 1
         return out
 
     def Free(self, t: Tensor) -> None:
@@ -354,7 +370,9 @@ class RocmBackend:
     def _dev_out(self, shape) -> Tensor:
         n = int(np.prod(shape)) * 4
         ptr = fakhip.alloc_call("fhip_malloc", max(n, 4))
-        return Tensor(Dtype.F32, Layout.RowMajor, list(shape), None, DevBuf(ptr, n), self)
+        # An async output: not Ready() until the next host fence (cuda.go:583-596).
+        return Tensor(Dtype.F32, Layout.RowMajor, list(shape), None,
+                      DevBuf(ptr, n, be=self, born_gen=self.fence_gen), self)
 
     def _matmul(self, w: Tensor, X: Tensor, P: int, shape) -> Tensor:
         out, in_ = w.Shape

@@ -69,8 +69,9 @@ const Tuning &tuning();
 // Registry of tiled weights: every repack records the buffer's format and shape, and the matmul
 // entries refuse a pointer that does not start a tiled weight of the format and shape asked for
 // (a raw GGUF upload or a stale pointer would otherwise produce plausible garbage). Any other
-// write through the ABI into a recorded range (copies, memsets, unpack/dequant outputs, frees)
-// drops the record; a device-to-device copy of a whole recorded weight records the copy.
+// write through the ABI into a recorded range (copies, memsets, the outputs of unpack, dequant,
+// quantize, matmul and MLP calls, frees) drops the record; a device-to-device copy of a whole
+// recorded weight records the copy.
 enum WeightKind { kWeightQ4K = 1, kWeightQ8_0 = 2, kWeightQ6K = 3 };
 void tag_weight(const void *p, size_t bytes, int kind, int out, int in);
 void untag_range(const void *p, size_t bytes);

@@ -50,6 +50,7 @@ int fhip_q4k_matmul_f32(const void *dPacked, const float *dX, float *dY, int out
   clear_error();
   if (int rc = check_matmul("fhip_q4k_matmul_f32", dPacked, dX, dY, out, in, P)) return rc;
   if (P == 0) return FHIP_OK;
+  untag_range(dY, (size_t)P * out * 4);
   return q4k_matmul_run(dPacked, dX, dY, out, in, P);
 }
 
@@ -82,6 +83,7 @@ int fhip_q4k_matmul_group_f32(const void *const *dPacked, float *const *dY, cons
     g.tile0[i + 1] = g.tile0[i] + q4k_tiles(out[i]);
   }
   if (P == 0) return FHIP_OK;
+  for (int i = 0; i < count; ++i) untag_range(dY[i], (size_t)P * out[i] * 4);
   if (P <= kGemvMaxTokens) return q4k_gemv_group(g, dX, in, P);
   for (int i = 0; i < count; ++i)
     if (int rc = q4k_matmul_run(dPacked[i], dX, dY[i], out[i], in, P)) return rc;

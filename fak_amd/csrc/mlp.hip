@@ -66,6 +66,7 @@ int fhip_q4k_mlp_f32(const void *dGate, const void *dUp, const void *dDown, cons
   if (int rc = check_mlp("fhip_q4k_mlp_f32", dGate, dUp, dDown, dX, dY, hidden, inter, P, true))
     return rc;
   if (P == 0) return FHIP_OK;
+  untag_range(dY, (size_t)P * hidden * 4);
   return run_mlp(dGate, dUp, dDown, dX, dY, hidden, inter, P, true);
 }
 
@@ -76,6 +77,7 @@ int fhip_q4k_mlp_q6down_f32(const void *dGate, const void *dUp, const void *dDow
                          P, false))
     return rc;
   if (P == 0) return FHIP_OK;
+  untag_range(dY, (size_t)P * hidden * 4);
   return run_mlp(dGate, dUp, dDownQ6, dX, dY, hidden, inter, P, false);
 }
 

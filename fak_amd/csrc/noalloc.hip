@@ -72,6 +72,7 @@ int fhip_q4k_matmul_noalloc_f32(const void *dPacked, const float *dX, float *dY,
                 kScratchBytes);
   void *base = nullptr;
   if (int rc = scratch_for_current_device(&base)) return rc;
+  untag_range(dY, (size_t)P * out * 4);
   ScratchScope scope(base, kScratchBytes);
   return q4k_matmul_run(dPacked, dX, dY, out, in, P);
 }

@@ -309,6 +309,7 @@ extern "C" int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, fl
   if (((uintptr_t)dX & 15) != 0)
     return fail(FHIP_EINVAL, "fhip_q4k_matmul_int8_f32: dX must be 16-byte aligned");
   if (int rc = check_weight("fhip_q4k_matmul_int8_f32", dPacked, kWeightQ4K, out, in)) return rc;
+  untag_range(dY, (size_t)P * out * 4);
   const int nblk = in / 256;
   const bool fused = P <= kFusedTokens;
   int8_t *qx = nullptr;

@@ -478,6 +478,7 @@ int fhip_q6k_matmul_f32(const void *dPacked, const float *dX, float *dY, int out
   if (((uintptr_t)dX & 15) || ((uintptr_t)dPacked & 15))
     return fail(FHIP_EINVAL, "fhip_q6k_matmul_f32: dX and dPacked must be 16-byte aligned");
   if (int rc = check_weight("fhip_q6k_matmul_f32", dPacked, kWeightQ6K, out, in)) return rc;
+  untag_range(dY, (size_t)P * out * 4);
   return q6k_gemv(dPacked, dX, dY, out, in, P);
 }
 

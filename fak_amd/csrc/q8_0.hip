@@ -425,6 +425,7 @@ int fhip_q8_0_matmul_f32(const void *dPacked, const float *dX, float *dY, int ou
   if (((uintptr_t)dX & 15) || ((uintptr_t)dPacked & 15))
     return fail(FHIP_EINVAL, "fhip_q8_0_matmul_f32: dX and dPacked must be 16-byte aligned");
   if (int rc = check_weight("fhip_q8_0_matmul_f32", dPacked, kWeightQ8_0, out, in)) return rc;
+  untag_range(dY, (size_t)P * out * 4);
   // The raw-GGUF Q8_0 path is a decode GEMV in the reference; longer batches run in 16-token
   // slices of the same kernel.
   for (int t0 = 0; t0 < P; t0 += 16) {

@@ -142,6 +142,10 @@ extern "C" int fhip_q8_quantize_f32(const float *dX, int8_t *dCodes, float *dSca
                              "(rows=%d in=%d block=%d)", rows, in, block);
   if ((!dX || !dCodes || !dScales) && rows > 0 && in > 0)
     return fail(FHIP_EINVAL, "fhip_q8_quantize_f32: null pointer");
+  if (rows > 0 && in > 0) {
+    untag_range(dCodes, (size_t)rows * in);
+    untag_range(dScales, (size_t)rows * (in / block) * 4);
+  }
   return launch_quantize(dX, dCodes, dScales, rows, in, block);
 }
 
@@ -159,6 +163,7 @@ extern "C" int fhip_q8_matmul_f32(const int8_t *dCodes, const float *dScales, co
   if (!dCodes || !dScales || !dX || !dY)
     return fail(FHIP_EINVAL, "fhip_q8_matmul_f32: null pointer");
   if (!aligned4(dCodes)) return fail(FHIP_EINVAL, "fhip_q8_matmul_f32: dCodes must be 4-byte aligned");
+  untag_range(dY, (size_t)P * out * 4);
   const int nblk = in / block;
   // activation codes and scales in the library workspace (calls on one library are serialized)
   const size_t qbytes = ((size_t)P * in + 255) & ~(size_t)255;

@@ -13,6 +13,7 @@
 #include <map>
 #include <mutex>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "common.hpp"
@@ -32,14 +33,37 @@ std::unordered_map<void *, size_t> g_live;  // ptr -> bucket bytes
 std::multimap<size_t, void *> g_free;       // bucket bytes -> parked ptr
 size_t g_free_bytes = 0;
 
-// One grow-only workspace per stream. Buffers outgrown (or left by a destroyed stream) are
-// retired, not freed: graphs captured earlier may still launch kernels that use them.
+// One grow-only workspace per stream. A buffer outgrown, or left by a destroyed stream, is freed
+// at once (after its stream drains) when no graph was ever captured on that stream; otherwise a
+// graph may still launch kernels that use it, so it is retired and freed by fhip_trim_pool once
+// no graph is alive.
 struct StreamWs {
   void *buf = nullptr;
   size_t bytes = 0;
 };
 std::unordered_map<hipStream_t, StreamWs> g_ws;
 std::vector<void *> g_ws_retired;
+std::unordered_set<hipStream_t> g_captured;  // streams a capture ever began on
+int g_live_graphs = 0;                       // instantiated graphs not yet destroyed
+bool g_capturing = false;                    // between fhip_graph_begin and fhip_graph_end
+
+// An instantiated graph and the stream it was captured on: its kernels use that stream's
+// workspace, so it replays only there.
+struct GraphHandle {
+  hipGraphExec_t exec;
+  hipStream_t stream;
+};
+
+// Give up a workspace buffer of stream s (see StreamWs).
+void release_ws(hipStream_t s, void *buf) {
+  if (!buf) return;
+  if (g_captured.count(s)) {
+    g_ws_retired.push_back(buf);
+    return;
+  }
+  (void)hipStreamSynchronize(s);
+  (void)hipFree(buf);
+}
 
 // The active ScratchScope, if any.
 void *g_scope_base = nullptr;
@@ -114,7 +138,7 @@ void *workspace(size_t bytes) {
   void *p = nullptr;
   hipError_t e = hipMalloc(&p, want);
   if (e != hipSuccess) { hip_fail(e, "workspace: hipMalloc"); return nullptr; }
-  if (w.buf) g_ws_retired.push_back(w.buf);
+  release_ws(g_stream, w.buf);
   w.buf = p;
   w.bytes = want;
   return w.buf;
@@ -265,6 +289,13 @@ void fhip_free(void *d) {
 
 void fhip_trim_pool(size_t max_keep_bytes) {
   std::lock_guard<std::mutex> lk(g_pool_mu);
+  // Retired workspaces: once no graph is alive (and none is being captured), nothing can launch
+  // kernels that use them; drained, they go back to the driver.
+  if (!g_ws_retired.empty() && g_live_graphs == 0 && !g_capturing) {
+    (void)hipDeviceSynchronize();
+    for (void *b : g_ws_retired) (void)hipFree(b);
+    g_ws_retired.clear();
+  }
   if (g_free_bytes <= max_keep_bytes) return;
   // Parked blocks may still be referenced by queued work: drain before releasing.
   (void)hipDeviceSynchronize();
@@ -356,12 +387,14 @@ int fhip_stream_destroy(void *s) {
   clear_error();
   if (!s) return FHIP_OK;
   if ((hipStream_t)s == g_stream) g_stream = nullptr;
-  // Its workspace is retired, not freed: a graph captured on the stream may still use it.
+  // Its workspace is freed once the stream drains, or retired if a graph captured on the stream
+  // may still use it.
   auto it = g_ws.find((hipStream_t)s);
   if (it != g_ws.end()) {
-    if (it->second.buf) g_ws_retired.push_back(it->second.buf);
+    release_ws((hipStream_t)s, it->second.buf);
     g_ws.erase(it);
   }
+  g_captured.erase((hipStream_t)s);
   FHIP_CHECK(hipStreamDestroy((hipStream_t)s));
   return FHIP_OK;
 }
@@ -383,7 +416,9 @@ int fhip_graph_begin(void) {
   if (!g_stream)
     return fail(FHIP_EINVAL, "fhip_graph_begin: capture needs a stream from fhip_stream_create "
                              "made current with fhip_set_stream");
+  g_captured.insert(g_stream);
   FHIP_CHECK(hipStreamBeginCapture(g_stream, hipStreamCaptureModeRelaxed));
+  g_capturing = true;
   return FHIP_OK;
 }
 
@@ -392,26 +427,38 @@ int fhip_graph_end(void **graph) {
   if (!graph) return fail(FHIP_EINVAL, "fhip_graph_end: null out pointer");
   *graph = nullptr;
   hipGraph_t g = nullptr;
+  g_capturing = false;
   FHIP_CHECK(hipStreamEndCapture(g_stream, &g));
   hipGraphExec_t ex = nullptr;
   const hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
   (void)hipGraphDestroy(g);
   if (e != hipSuccess) return hip_fail(e, "fhip_graph_end: hipGraphInstantiate");
-  *graph = (void *)ex;
+  *graph = new GraphHandle{ex, g_stream};
+  ++g_live_graphs;
   return FHIP_OK;
 }
 
 int fhip_graph_launch(void *graph) {
   clear_error();
   if (!graph) return fail(FHIP_EINVAL, "fhip_graph_launch: null graph");
-  FHIP_CHECK(hipGraphLaunch((hipGraphExec_t)graph, g_stream));
+  const GraphHandle *h = static_cast<const GraphHandle *>(graph);
+  // Its kernels use the scratch of the stream they were captured on; replayed on another
+  // stream they would race with work queued there.
+  if (h->stream != g_stream)
+    return fail(FHIP_EINVAL, "fhip_graph_launch: a graph replays only on the stream it was "
+                             "captured on; make that stream current with fhip_set_stream");
+  FHIP_CHECK(hipGraphLaunch(h->exec, h->stream));
   return FHIP_OK;
 }
 
 int fhip_graph_destroy(void *graph) {
   clear_error();
   if (!graph) return FHIP_OK;
-  FHIP_CHECK(hipGraphExecDestroy((hipGraphExec_t)graph));
+  GraphHandle *h = static_cast<GraphHandle *>(graph);
+  const hipError_t e = hipGraphExecDestroy(h->exec);
+  delete h;
+  --g_live_graphs;
+  if (e != hipSuccess) return hip_fail(e, "fhip_graph_destroy: hipGraphExecDestroy");
   return FHIP_OK;
 }
 

@@ -353,7 +353,11 @@ std::vector<float> RocmBackend::Read(const Tensor &t) {
   const DeviceBuffer *db = t.device();
   if (!db || !db->ptr) throw std::invalid_argument("compute: rocm Read of a non-resident tensor");
   std::vector<float> out((size_t)t.Numel());
-  if (!out.empty()) check("fhip_d2h", fhip_d2h(out.data(), db->ptr, out.size() * 4));
+  if (!out.empty()) {
+    check("fhip_d2h", fhip_d2h(out.data(), db->ptr, out.size() * 4));
+    // The copy drained the stream: everything enqueued before it is materialized (cuda.go:896).
+    fence_gen_->fetch_add(1);
+  }
   return out;
 }
 
@@ -383,6 +387,9 @@ Tensor RocmBackend::dev_out(std::vector<int> shape) {
   auto db = std::make_shared<DeviceBuffer>();
   db->bytes = (size_t)r.Numel() * 4;
   db->ptr = alloc(db->bytes);
+  // An async output: not Ready() until the next host fence (cuda.go:583-596).
+  db->fence = fence_gen_;
+  db->born_gen = fence_gen_->load();
   r.buf = db;
   r.be = this;
   return r;

@@ -13,6 +13,7 @@
 // f32 GEMMs belong to other kernels and throw std::logic_error.
 #pragma once
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 #include <memory>
@@ -69,11 +70,19 @@ struct HostBuffer : Buffer {
 };
 
 // A device allocation from the fakhip pool. HAL Q8 weights carry a second (scales) buffer.
+// An async op output (a matmul result) records the fence generation it was enqueued in and is
+// Ready() only once a host fence (Read) has bumped its backend's generation past it
+// (cudaBuf.Ready, internal/compute/cuda.go:286-300): the stream is FIFO, so one fence
+// materializes every buffer enqueued before it. Buffers with no fence counter (uploads, which
+// complete before they return) are always ready.
 struct DeviceBuffer : Buffer {
   void *ptr = nullptr;
   size_t bytes = 0;
   void *scales = nullptr;
   int block = 0;
+  std::shared_ptr<const std::atomic<uint64_t>> fence;
+  uint64_t born_gen = 0;
+  bool Ready() const override { return !fence || fence->load() > born_gen; }
 };
 
 class Backend;
@@ -180,6 +189,9 @@ class RocmBackend : public Backend {
     Dtype dtype;
     Tensor t;
   };
+  // Host fences (Read) so far (cudaBackend.fenceGen, cuda.go:327-331); shared with the async
+  // outputs so their Ready() stays valid after the backend is gone.
+  std::shared_ptr<std::atomic<uint64_t>> fence_gen_ = std::make_shared<std::atomic<uint64_t>>(0);
   std::vector<CacheEntry> cache_;
   std::string tier_;
   bool kq_int8_ = false;

@@ -26,8 +26,9 @@
  *     The library records the format and shape of every tiled weight it lays out; the matmul,
  *     unpack and dequant entries return FHIP_EINVAL for a pointer that does not start a tiled
  *     weight of the format and [out, in] they are given (raw GGUF bytes, another shape, a freed
- *     or overwritten buffer). Writing into a tiled weight through fhip_h2d / fhip_h2d_async /
- *     fhip_memset_async / a partial fhip_d2d, or freeing it, drops the record; an fhip_d2d of a
+ *     or overwritten buffer). Writing into a tiled weight through any entry (fhip_h2d /
+ *     fhip_h2d_async / fhip_memset_async / a partial fhip_d2d, the output of an unpack,
+ *     dequant, quantize, matmul or MLP call), or freeing it, drops the record; an fhip_d2d of a
  *     whole tiled weight records the copy as the same weight.
  *   - Launch-shape overrides (FAK_HIP_GEMV_TW/_KW, FAK_HIP_GEMV_GLOBALX, FAK_HIP_GEMV16_FROM,
  *     FAK_HIP_GEMM32_FORM/_SK/_NWB, FAK_HIP_I8R_KW, FAK_HIP_Q8_TW/_KW) are read from the
@@ -81,8 +82,10 @@ int fhip_memset_async(void *d, int value, size_t bytes);
 /* Streams and events (the CUDA tenant has one global g_stream, cuda_kernels.cu:28-32; this
  * backend exposes the stream as a handle so a host can overlap work or capture graphs).
  * Streams are created at the default priority. Each stream gets its own scratch workspace on
- * first use; destroying a stream retires (does not free) it, since a graph captured on the
- * stream may still use it. */
+ * first use. Destroying a stream (or outgrowing its workspace) frees the buffer once the stream
+ * has drained; if a graph was ever captured on the stream the buffer is kept instead, since the
+ * graph's kernels may still use it, and fhip_trim_pool frees such buffers once no graph is
+ * alive. */
 int fhip_stream_create(void **stream);
 int fhip_stream_destroy(void *stream);
 /* Make `stream` (NULL = the default stream) the target of every later launch and async copy. */
@@ -94,7 +97,9 @@ int fhip_stream_sync(void *stream);
  * made: the *_matmul_f32 / *_group_f32 entries and fhip_q8_quantize_f32 (no fhip_malloc, no
  * synchronous copies, no fhip_memset_async: memset nodes are not allowed in these graphs). Run
  * each call once before capture so the library workspace already has its size. A graph replays
- * the captured launches on the current stream with the same device pointers. */
+ * the captured launches with the same device pointers on the stream it was captured on, which
+ * must be current (fhip_graph_launch returns FHIP_EINVAL otherwise: its kernels use that
+ * stream's workspace and would race with work queued there). */
 int fhip_graph_begin(void);
 int fhip_graph_end(void **graph);
 int fhip_graph_launch(void *graph);
@@ -153,10 +158,16 @@ int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, float *dY, in
  * reference. It runs the kernels of fhip_q4k_matmul_f32 (same results, bit for bit) but keeps
  * their scratch (activation operands, token scales, K-range partial sums) in a static 64 MiB
  * device array per device instead of the library workspace, and calls no hipMalloc / hipFree.
- * A call whose scratch would exceed 64 MiB returns FHIP_EINVAL without launching anything
- * (every GEMV of up to 16 tokens fits, and so does a prefill of 512 tokens at the 7B shapes; a
- * prefill of 1,024 tokens through the 18944 -> 3584 projection does not). The array keeps the last call's contents and is shared by every call on the device: calls that
- * overlap on one device (two streams, two threads) race on it. */
+ * A call whose scratch would exceed 64 MiB returns FHIP_EINVAL without launching anything.
+ * The scratch is: for 1..4 tokens at most in/256 * 3.3 KB; for 5..32 tokens (3..32 when
+ * in >= 24576) the K-range partial sums, 4 * P * out bytes per 1,024 values of in (about
+ * in * out * P / 256 bytes); for the prefill GEMM its f16 operands (2 * P * in bytes) plus
+ * partial sums when K is split. So every 7B / 27B FFN, attention and 152064 x 3584 lm_head
+ * call of up to 32 tokens fits, and so does a prefill of 512 tokens at the 7B shapes; a
+ * 16-token call on a 17408 x 65536 weight (71 MB) and a 1,024-token prefill through the
+ * 18944 -> 3584 projection do not. The array keeps the last call's contents and is shared by
+ * every call on the device: calls that overlap on one device (two streams, two threads) race on
+ * it. */
 int fhip_q4k_matmul_noalloc_f32(const void *dPacked, const float *dX, float *dY, int out, int in,
                                 int P);
 

@@ -251,6 +251,37 @@ void cpu_cases(bool need_device) {
 void gpu_cases() {
   RocmBackend cb(0);
 
+  // cudaBuf.Ready (internal/compute/cuda.go:286-300): an async op output is not ready until a
+  // host fence (Read) bumps the fence generation past the one it was enqueued in; one fence
+  // materializes every buffer enqueued before it; uploads are ready on return.
+  run("AsyncOutputsReadyAfterFence", [&] {
+    Lcg g{0x4b4b};
+    const int out = 320, in = 256;
+    const auto raw = rand_q4k_bytes(g, out, in);
+    Tensor wq = cb.Upload(NewQ4K(&cb, {out, in}, raw), Dtype::Q4_K);
+    EXPECT(wq.buf->Ready(), "an uploaded weight is ready");
+    std::vector<float> x(in);
+    for (int i = 0; i < in; ++i) x[i] = g.f();
+    Tensor xd = resident(cb, {in}, x);
+    EXPECT(xd.buf->Ready(), "an uploaded activation is ready");
+    Tensor y1 = cb.MatMul(wq, xd);
+    Tensor y2 = cb.MatMul(wq, xd);
+    EXPECT(!y1.buf->Ready() && !y2.buf->Ready(), "fresh matmul outputs are not ready");
+    const auto r2 = cb.Read(y2);
+    EXPECT(y1.buf->Ready() && y2.buf->Ready(),
+           "a Read fences every output enqueued before it");
+    Tensor y3 = cb.MatMul(wq, xd);
+    EXPECT(!y3.buf->Ready(), "an output enqueued after the fence is not ready");
+    const auto r3 = cb.Read(y3);
+    EXPECT(y3.buf->Ready(), "ready after its own Read");
+    EXPECT(r2 == r3, "same inputs, same bits");
+    cb.Free(y1);
+    cb.Free(y2);
+    cb.Free(y3);
+    cb.Free(xd);
+    cb.Free(wq);
+  });
+
   run("Q4KMatMulApproxMatchesRef", [&] {
     Lcg g{0x4b4b};
     const int out = 320, in = 256;

@@ -36,6 +36,30 @@ def test_registry_and_caps(be):
     assert be.Tier() == "gfx950"
 
 
+def test_async_outputs_ready_after_fence(be):
+    """cudaBuf.Ready (internal/compute/cuda.go:286-300): Caps.Async is advertised, so a matmul
+    output is not Ready() until a host fence (Read) bumps the fence generation past the one it
+    was enqueued in; one fence materializes every output enqueued before it; uploads are ready
+    on return."""
+    assert be.Caps().Async
+    g = fx.LCG(0x4B4B)
+    out, in_ = 320, 256
+    wq = be.Upload(B.NewQ4K(be, [out, in_], fx.rand_q4k_bytes(g, out, in_)), B.Dtype.Q4_K)
+    xd = be.Upload(B.NewF32(be, [in_], np.linspace(-1, 1, in_, dtype=np.float32)))
+    assert wq.buf.Ready() and xd.buf.Ready()
+    y1, y2 = be.MatMul(wq, xd), be.MatMul(wq, xd)
+    assert not y1.buf.Ready() and not y2.buf.Ready()
+    r2 = be.Read(y2)
+    assert y1.buf.Ready() and y2.buf.Ready()
+    y3 = be.MatMul(wq, xd)
+    assert not y3.buf.Ready()
+    r3 = be.Read(y3)
+    assert y3.buf.Ready()
+    assert np.array_equal(r2.view(np.uint32), r3.view(np.uint32))
+    for t in (y1, y2, y3, xd):
+        be.Free(t)
+
+
 def test_q4k_matmul_witness(be, oracle_mod):
     """TestCUDAQ4KMatMulApproxMatchesRef on this backend."""
     print("[case] backend Q4_K MatMul witness", flush=True)

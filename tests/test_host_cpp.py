@@ -40,5 +40,5 @@ def test_host_cpp_backend_on_device():
     assert r.returncode == 0, r.stdout
     for case in ("Q4KMatMulApproxMatchesRef", "Q4KBatchedMatMulApproxMatchesRef",
                  "Q8MatMulApproxMatchesRef", "Q8BatchedMatMulApproxMatchesRef", "QuantVRAMWitness",
-                 "Q4KInt8RouteBitIdentical", "FusedMLPMatchesChain"):
+                 "Q4KInt8RouteBitIdentical", "FusedMLPMatchesChain", "AsyncOutputsReadyAfterFence"):
         assert f"PASS {case}" in r.stdout

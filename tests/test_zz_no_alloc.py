@@ -19,11 +19,15 @@ def run(fn, w, X, out, in_, P):
 
 # (out, in, P): a K-split prefill GEMM (operands + token scales + partials: ~56 MB of scratch),
 # then smaller calls: a 16-token GEMV with K-range partials, a 3-token GEMV with global
-# activation operands, one decode token.
-CALLS = [(3584, 18944, 512), (2048, 6144, 16), (3584, 18944, 3), (1024, 3584, 1)]
+# activation operands, one decode token, a 24-token call (the 17..32-token route, K-range
+# partials sized for its tokens) and a 4-token call at in >= 24576 (which takes the 5..16-token
+# kernel's route from three tokens).
+CALLS = [(3584, 18944, 512), (2048, 6144, 16), (3584, 18944, 3), (1024, 3584, 1),
+         (18944, 3584, 24), (5120, 25600, 4)]
 
 
-@pytest.mark.parametrize("first,second", [(0, 1), (1, 2), (2, 3), (0, 3)])
+@pytest.mark.parametrize("first,second", [(0, 1), (1, 2), (2, 3), (0, 3), (0, 4), (4, 5),
+                                          (5, 3)])
 def test_noalloc_matches_allocating_entry(hip, oracle_mod, first, second):
     lib = fakhip.load()
     for idx in (first, second):
@@ -59,3 +63,28 @@ def test_noalloc_refuses_oversized_scratch(hip):
                 fakhip.EINVAL
     finally:
         lib.fhip_free(w)
+
+
+def test_noalloc_refuses_wide_head_at_16_tokens(hip):
+    """The 5..32-token routes keep K-range partial sums of about 4 * P * out bytes per 1,024
+    values of in: at 16 tokens a [17408, 65536] weight needs 71.3 MB, beyond the 64 MiB array, so
+    the call is refused before any launch (the weight is laid out from zero bytes on the device:
+    no host data of that size is needed)."""
+    lib = fakhip.load()
+    out, in_, P = 17408, 65536, 16
+    nbytes = out * (in_ // 256) * 144
+    with Dev(nbytes) as raw:
+        fakhip.call("fhip_memset_async", raw.ptr, 0, nbytes)
+        fakhip.call("fhip_sync")
+        w = fakhip.alloc_call("fhip_malloc", lib.fhip_q4k_packed_bytes(out, in_))
+        try:
+            fakhip.call("fhip_q4k_repack", w, raw.ptr, out, in_)
+            with Dev(P * in_ * 4) as dx, Dev(P * out * 4) as dy:
+                assert lib.fhip_q4k_matmul_noalloc_f32(w, dx.ptr, dy.ptr, out, in_, P) == \
+                    fakhip.EINVAL
+                assert "static region" in fakhip.last_error()
+                # 4 tokens of the same weight need only a little scratch: accepted.
+                fakhip.call("fhip_q4k_matmul_noalloc_f32", w, dx.ptr, dy.ptr, out, in_, 4)
+                fakhip.call("fhip_sync")
+        finally:
+            lib.fhip_free(w)
