@@ -47,7 +47,7 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16 MFMA
 ROTATE_BYTES = 300 << 20    # > 256 MB Infinity Cache
 MIN_COPIES = 9              # at least this many distinct weight copies per rotating workload
-CPU_THREADS_MAX = 16        # the host-CPU share of one GPU on the benchmark boxes
+CPU_THREADS_MAX = 16        # worker-pool cap: the host-CPU share of one GPU on the benchmark boxes
 METRIC = "Q4_K decode GEMV HBM GB/s (% peak); prefill GEMM TFLOP/s (% MFMA peak)"
 
 
@@ -148,6 +148,20 @@ def sample_rows(raw, n, k, rows):
     """The first and last rows/2 rows of a raw Q4_K weight: (sub-weight bytes, row indices)."""
     rb = (k // 256) * 144
     sel = np.concatenate([np.arange(0, rows // 2), np.arange(n - rows // 2, n)])
+    return np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel]), sel
+
+
+def spread_sample(raw, n, k, per_block=2, block=128):
+    """Rows of a raw Q4_K weight that touch every 128-row block of the output (the GEMM's row
+    tile), per_block rows per block at offsets that vary from block to block, plus the first and
+    last row: (sub-weight bytes, row indices)."""
+    rows = {0, n - 1}
+    for b in range(0, n, block):
+        size = min(block, n - b)
+        for j in range(per_block):
+            rows.add(b + (37 * (b // block) + 61 * j + 5 * j * j) % size)
+    sel = np.array(sorted(rows))
+    rb = (k // 256) * 144
     return np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel]), sel
 
 
@@ -307,7 +321,7 @@ def bench_q8_0(steps, warmup, ev, graph_copies=300):
 
 def bench_gemm(M, steps, warmup, ev):
     """C3: prefill GEMM K=3584 -> N=18944 at M tokens, weights rotating over >= 9 copies;
-    checked on 256 sampled output rows."""
+    checked on 297 output rows spread over all 148 row blocks."""
     n, k = 18944, 3584
     w = Weight("q4k", n, k, 3, copies_for(q4k_bytes(n, k)))
     X = synth.activations(M, k, 4)
@@ -318,7 +332,7 @@ def bench_gemm(M, steps, warmup, ev):
     t = ms * 1e-3  # back to back: one call per step
     import oracle  # the checker
     fakhip.call("fhip_q4k_matmul_f32", w.ptrs[0], xb.ptr, yb.ptr, n, k, M)
-    sub, sel = sample_rows(w.raw, n, k, 256)
+    sub, sel = spread_sample(w.raw, n, k)
     chk = check(yb.host().reshape(M, n)[:, sel], oracle.q4k_gemm(sub, len(sel), k, X, M,
                                                                   workers=cpu_threads()))
     res = {"M": M, "us_per_call": 1e3 * per[0], "us_back_to_back": 1e3 * ms,
@@ -611,14 +625,19 @@ def bench_decode_stack(steps, warmup, ev, layers=28):
 
 
 
-def cpu_threads():
-    """Threads of the CPU legs: the cores this process may run on, at most the 16-core host share
-    that one GPU has on the benchmark boxes."""
+def nproc():
+    """The cores this process may run on (what `nproc` prints)."""
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(n, CPU_THREADS_MAX))
+        return os.cpu_count() or 1
+
+
+def cpu_threads():
+    """Threads of the CPU legs: nproc, the reference's worker count (parallel.go:31-34), capped at
+    the 16-core host share one GPU has on the benchmark boxes (the cap binds only where more
+    cores are visible than that share)."""
+    return max(1, min(nproc(), CPU_THREADS_MAX))
 
 
 def cpu_model():
@@ -658,7 +677,7 @@ def cpu_baselines(c2_in, c1_in=None, c3_in=None, c4_in=None, c5_in=None):
     base = {"value": alg2 / t / 1e9, "unit": "GB/s", "cores": W, "kind": "port",
             "sample": f"full C2 pair (gate/up 3584->18944 + down 18944->3584, M=1), median of "
                       f"{reps} after a warm-up: {t * 1e3:.2f} ms",
-            "host_cpus_visible": os.cpu_count(), "cpu_model": cpu_model(),
+            "nproc": nproc(), "host_cpus_visible": os.cpu_count(), "cpu_model": cpu_model(),
             "build": "gcc -O3 -ffp-contract=off -fno-fast-math (oracle/build.py)"}
     cfg = {"c2_q4k_gemv_pair": {"GBs": round(base["value"], 2), "ms_per_step": t * 1e3}}
     if c1_in is not None:
@@ -741,9 +760,10 @@ def main():
         "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(c2["ms_per_step"], 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8",
-        "arithmetic": "Q4_K 4-bit codes x activations carried as two int8 digits per value "
-                      "(a power-of-two scale per 32 values) on v_mfma_i32_16x16x64_i8 with exact "
-                      "int32 sums; sub-block scales, mins and accumulation in f32",
+        "arithmetic": "Q4_K 4-bit codes x activations carried as three int8 digits per value "
+                      "(a power-of-two scale per 32 values, 2^-17 of the scale) on "
+                      "v_mfma_i32_16x16x64_i8 with exact int32 sums; sub-block scales, mins and "
+                      "accumulation in f32",
         "data": "synthetic (seeded GGUF Q4_K blocks, N(0,1) activations)",
         "config": {"workload": "Q4_K decode GEMV M=1, Qwen2.5-7B FFN: gate/up K=3584 N=18944 + "
                                "down K=18944 N=3584", "M": 1,

@@ -31,6 +31,19 @@ def rel_err_rows(got: np.ndarray, ref: np.ndarray) -> float:
     return max(rel_err(g, r) for g, r in zip(got, ref))
 
 
+def spread_rows(n: int, per_block: int = 2, block: int = 128) -> np.ndarray:
+    """Row indices for a sampled check of an n-row output that touch every block of `block` rows
+    (the GEMM's row tile; each 16-row tile of the GEMV lies in one): `per_block` rows per block
+    at offsets that differ from block to block (so every lane position is exercised over the
+    blocks), plus the first and last row."""
+    rows = {0, n - 1}
+    for b in range(0, n, block):
+        size = min(block, n - b)
+        for j in range(per_block):
+            rows.add(b + (37 * (b // block) + 61 * j + 5 * j * j) % size)
+    return np.array(sorted(rows))
+
+
 def scaled_activations(P: int, K: int, seed: int, pattern: str) -> np.ndarray:
     """N(0,1) activations reshaped to stress the activation scaling of every route:
     'big' rows x 1e5 (beyond f16), 'tiny' rows x 1e-20 (below f16), 'wee' rows x 1e-35 (block

@@ -7,14 +7,14 @@ inputs, at the reference's tolerances (metric of internal/model/quant_q4k_test.g
 
 Shapes: the five workloads (Q8_0 576->1536; Q4_K 3584->18944 and 18944->3584; prefill
 M=128/512/2048 at 3584->18944; 27B-class 5120<->25600 at M=1,4,8,16) plus small/ragged shapes
-and the reference's witness shapes. Full-size GEMMs are checked on a sample of output rows (the
-oracle cost is per row), everything else on every output.
+and the reference's witness shapes. Full-size GEMMs are checked on sampled output rows spread
+over every 128-row block (the oracle cost is per row), everything else on every output.
 """
 import numpy as np
 import pytest
 
 from fak_amd import synth
-from tests.gpu_util import cosine, knobs, q4k_matmul, q8_0_matmul, rel_err
+from tests.gpu_util import cosine, knobs, q4k_matmul, q8_0_matmul, rel_err, spread_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -32,8 +32,9 @@ def _check_q4k(oracle_mod, out, in_, P, seed, tol, workers=16, rows=None):
         ref = oracle_mod.q4k_gemm(raw, out, in_, X, P, workers=workers)
         got = Y
     else:
+        # `rows` is a budget: at least two rows in every 128-row block
         rb = (in_ // 256) * 144
-        sel = np.concatenate([np.arange(0, rows // 2), np.arange(out - rows // 2, out)])
+        sel = spread_rows(out, per_block=max(2, rows // -(-out // 128)))
         sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
         ref = oracle_mod.q4k_gemm(sub, len(sel), in_, X, P, workers=workers)
         got = Y[:, sel]
@@ -233,7 +234,8 @@ def test_q4k_small_prefill_activation_scales(hip, oracle_mod, pattern):
 
 @pytest.mark.parametrize("P", [128, 512, 2048])
 def test_q4k_gemm_prefill_7b(hip, oracle_mod, P):
-    """Prefill GEMM at M=128/512/2048, K=3584, N=18944 (sampled output rows)."""
+    """Prefill GEMM at M=128/512/2048, K=3584, N=18944, checked on two output rows in every
+    one of the 148 row blocks (296 rows)."""
     _check_q4k(oracle_mod, 18944, 3584, P, seed=512 + P, tol=GEMM_TOL, rows=256)
 
 
@@ -261,7 +263,7 @@ def test_q4k_gemm_forms_bit_identical(hip, oracle_mod, monkeypatch, out, in_, P)
     assert np.array_equal(Y2.view(np.uint32), Y4.view(np.uint32))
     if out > 4096:
         rb = (in_ // 256) * 144
-        sel = np.concatenate([np.arange(0, 128), np.arange(out - 128, out)])
+        sel = spread_rows(out)
         sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
         ref = oracle_mod.q4k_gemm(sub, len(sel), in_, X, P, workers=16)
         got = Y3[:, sel]
@@ -284,7 +286,7 @@ def test_q4k_gemm_k_split(hip, oracle_mod, out, in_, P):
     assert np.array_equal(Y.view(np.uint32), q4k_matmul(raw, out, in_, X, P).view(np.uint32))
     if out * in_ > 4_000_000:
         rb = (in_ // 256) * 144
-        sel = np.concatenate([np.arange(0, 32), np.arange(out - 32, out)])
+        sel = spread_rows(out, per_block=1)
         sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
         ref = oracle_mod.q4k_gemm(sub, len(sel), in_, X, P, workers=16)
         got = Y[:, sel]

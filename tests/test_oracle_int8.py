@@ -7,10 +7,13 @@ quantizeRowQ8scalar (internal/model/quant_quantize.go:16-43).
   * the combine against a closed form on integer-exact inputs (d = dmin = 1, dx = 1);
   * the float chain's order against hand-derived cancellation cases (tests/int8_cases.py);
   * TestQ4KInt8DotMatchesF32 (internal/model/quant_q4k_int8_test.go:16-60): max|int8 - f32| / RMS
-    <= 0.05 against the f32 route on random blocks, out = 48, in = 768.
-What no check here fixes is the association inside one term, (f32(I) * ws) * dx: it follows the
-source text (Go evaluates left to right and never fuses on amd64).
+    <= 0.05 against the f32 route on random blocks, out = 48, in = 768;
+  * the association inside one term, (f32(I) * ws) * dx (quant_q4k_int8.go:122: Go evaluates
+    left to right and never fuses on amd64), on a term where the other association rounds to a
+    different f32, the expected value derived with exact rational arithmetic.
 """
+import fractions
+import struct
 import numpy as np
 import pytest
 
@@ -66,6 +69,47 @@ def test_combine_order_cases(oracle_mod):
     raw, x, want = ic.order_cases()
     y = oracle_mod.q4k_matrows_int8(raw, 3, 256, x)
     np.testing.assert_array_equal(y, want)
+
+
+def _round_f32(q: fractions.Fraction) -> float:
+    """The f32 nearest to the rational q (ties to even), for normal-range q."""
+    if q == 0:
+        return 0.0
+    sign = -1 if q < 0 else 1
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while fractions.Fraction(2) ** e > a:
+        e -= 1
+    while fractions.Fraction(2) ** (e + 1) <= a:
+        e += 1
+    ulp = fractions.Fraction(2) ** (e - 23)  # 24-bit significand
+    n, r = divmod(a, ulp)
+    if r * 2 > ulp or (r * 2 == ulp and n % 2 == 1):
+        n += 1
+    return sign * float(n * ulp)
+
+
+def test_combine_term_association(oracle_mod):
+    """One sub-block term, I = 7305, d = f16 0x3EE5 (1.7236328125), sc = 59, dx = 0x3AA69B6D
+    (dmin = 0, so the min term is zero): (f32(I) * ws) * dx rounds to 944.27966..., the other
+    association f32(I) * (ws * dx) to 944.27972...; the oracle must give the first."""
+    d_bits, sc, I = 0x3EE5, 59, 7305
+    dx = struct.unpack("<f", struct.pack("<I", 0x3AA69B6D))[0]
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.frombuffer(struct.pack("<H", d_bits), np.uint8)
+    scm = np.zeros(8, np.uint8)
+    scm[0] = sc
+    blk[4:16] = synth.pack_scale_min_k4(scm[None, :], np.zeros((1, 8), np.uint8))[0]
+    F = fractions.Fraction
+    d = F(struct.unpack("<e", struct.pack("<H", d_bits))[0])
+    ws = _round_f32(d * sc)
+    go = _round_f32(F(_round_f32(F(I) * F(ws))) * F(dx))
+    alt = _round_f32(F(I) * F(_round_f32(F(ws) * F(dx))))
+    assert go != alt  # the case separates the two associations
+    IS = np.zeros(8, np.int32)
+    IS[0] = I
+    got = oracle_mod.q4k_combine_row(blk, 1, np.full(8, dx, np.float32), IS, np.zeros(8, np.int32))
+    assert got == go, (got, go, alt)
 
 
 def test_int8_route_close_to_f32(oracle_mod):
