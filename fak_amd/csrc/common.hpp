@@ -47,6 +47,10 @@ class ScratchScope {
 // device (noalloc.hip); called by fhip_init.
 int noalloc_setup();
 
+// Events set by fhip_time_next_launch, handed to (and cleared by) the next launch that takes
+// them (the one-token GEMV); both null when none are pending.
+void take_launch_events(hipEvent_t *start, hipEvent_t *stop);
+
 // Device properties cached by fhip_init.
 int cu_count();
 // Largest dynamic LDS allocation one workgroup may request (bytes).

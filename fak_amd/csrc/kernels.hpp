@@ -47,6 +47,8 @@ int q6k_gemv16(const void *W, const float *X, float *Y, int N, int K, int M);
 // Fused decode MLP pieces (1..4 tokens): the workspace a small-M call over `ntiles` tiles
 // needs, the SwiGLU stage over {gate, up}, and the Q6_K GEMV.
 size_t gemv_i8_ws_bytes(int ntiles, int K, int M, bool swiglu);
+// The one-token GEMV's workgroup shape over `ntiles` 16-row tiles of reduction dim K.
+void q4k_gemv1_shape(int ntiles, int K, int &TW, int &KW);
 int q4k_gemv_swiglu(const void *gate, const void *up, const float *X, float *inter, int I, int K,
                     int M, void *ws);
 int q6k_gemv(const void *W, const float *X, float *Y, int N, int K, int M);

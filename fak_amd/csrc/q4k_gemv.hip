@@ -49,6 +49,8 @@
 // interleaved (gate tile T, up tile T, gate tile T + 1, ...) and TW even, so both tiles of a row
 // block sit in one workgroup; the gate tile's final wave writes silu(gate) * up for its rows
 // instead of two separate outputs.
+#include <hip/hip_ext.h>
+
 #include "gemv_common.hpp"
 
 namespace fhip {
@@ -795,9 +797,14 @@ int launch_i8(const GemvGroup &g, const float *X, int K, int M, bool swiglu, voi
     FHIP_CHECK_LAUNCH("gemv_i8_prep_kernel");
     xg = xop;
   }
+  // The kernel goes out through hipExtLaunchKernelGGL so that fhip_time_next_launch's events
+  // (null otherwise, an ordinary launch) take the dispatch's own start and end timestamps.
+  hipEvent_t ev0, ev1;
+  take_launch_events(&ev0, &ev1);
 #define FHIP_I8_LAUNCH_EX(LXV, SWV, XMV, PF0V, EXV)                                          \
-  q4k_gemv_i8_kernel<MP, LXV, SWV, XMV, PF0V, EXV><<<grid, threads, p.lds_bytes, stream()>>>( \
-      g, X, xg, K, M, nblk, p.TW, p.KW)
+  hipExtLaunchKernelGGL(q4k_gemv_i8_kernel<MP, LXV, SWV, XMV, PF0V, EXV>, dim3(grid),        \
+                        dim3(threads), (uint32_t)p.lds_bytes, stream(), ev0, ev1, 0u, g, X, xg, \
+                        K, M, nblk, p.TW, p.KW)
 #define FHIP_I8_LAUNCH(LXV, SWV, XMV, PF0V)                                                  \
   do {                                                                                       \
     if (exact) FHIP_I8_LAUNCH_EX(LXV, SWV, XMV, PF0V, (MP > 1));                             \
@@ -875,6 +882,13 @@ size_t gemv_i8_ws_bytes(int ntiles, int K, int M, bool swiglu) {
            : M == 2 ? plan_i8<2>(ntiles, K, swiglu)
                     : plan_i8<4>(ntiles, K, swiglu);
   return p.xop_bytes;
+}
+
+// The one-token launch shape (TW tiles x KW waves per workgroup) over `ntiles` tiles.
+void q4k_gemv1_shape(int ntiles, int K, int &TW, int &KW) {
+  const I8Plan p = plan_i8<1>(ntiles, K, false);
+  TW = p.TW;
+  KW = p.KW;
 }
 
 // Scratch bytes of a 1..16-token Q4_K matmul of an [N, K] weight (the route q4k_gemv takes).

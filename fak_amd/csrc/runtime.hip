@@ -65,6 +65,9 @@ void release_ws(hipStream_t s, void *buf) {
   (void)hipFree(buf);
 }
 
+// fhip_time_next_launch's events, pending for the next launch that takes them.
+hipEvent_t g_next_start = nullptr, g_next_stop = nullptr;
+
 // The active ScratchScope, if any.
 void *g_scope_base = nullptr;
 size_t g_scope_cap = 0;
@@ -110,6 +113,16 @@ int lds_limit() { return g_lds; }
 const Tuning &tuning() { return g_tuning; }
 
 void clear_error() { g_err[0] = 0; }
+
+void take_launch_events(hipEvent_t *start, hipEvent_t *stop) {
+  if (g_capturing) {  // a captured launch takes none: the pair waits for the next eager launch
+    *start = *stop = nullptr;
+    return;
+  }
+  *start = g_next_start;
+  *stop = g_next_stop;
+  g_next_start = g_next_stop = nullptr;
+}
 
 int fail(int code, const char *fmt, ...) {
   va_list ap;
@@ -482,6 +495,15 @@ int fhip_event_record(void *ev) {
   clear_error();
   if (!ev) return fail(FHIP_EINVAL, "fhip_event_record: null event");
   FHIP_CHECK(hipEventRecord((hipEvent_t)ev, g_stream));
+  return FHIP_OK;
+}
+
+int fhip_time_next_launch(void *start, void *stop) {
+  clear_error();
+  if (!start || !stop) return fail(FHIP_EINVAL, "fhip_time_next_launch: null event");
+  if (g_capturing) return fail(FHIP_EINVAL, "fhip_time_next_launch: not during graph capture");
+  g_next_start = (hipEvent_t)start;
+  g_next_stop = (hipEvent_t)stop;
   return FHIP_OK;
 }
 

@@ -57,8 +57,13 @@ SIGNATURES = {
     "fhip_event_create": (_i, [C.POINTER(_vp)]),
     "fhip_event_destroy": (_i, [_vp]),
     "fhip_event_record": (_i, [_vp]),
+    "fhip_time_next_launch": (_i, [_vp, _vp]),
     "fhip_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(C.c_float)]),
     "fhip_q4k_packed_bytes": (_sz, [_i, _i]),
+    "fhip_probe_read_sink_words": (_sz, [_sz]),
+    "fhip_probe_read": (_i, [_vp, _sz, _vp]),
+    "fhip_probe_q4k_records_sink_words": (_sz, [_i, _i]),
+    "fhip_probe_q4k_records": (_i, [_vp, _i, _i, _vp]),
     "fhip_q4k_repack": (_i, [_vp, _vp, _i, _i]),
     "fhip_q4k_unpack": (_i, [_vp, _vp, _i, _i]),
     "fhip_q4k_dequant_f32": (_i, [_vp, _vp, _i, _i]),

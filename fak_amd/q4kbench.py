@@ -3,9 +3,12 @@ tokens, a number of repetitions, median-free plain timing with HIP events, and a
 Used as the target program for rocprofv3 runs (kernel trace, counters) on one shape.
 
     python -m fak_amd.q4kbench --n 18944 --k 3584 --m 1 --reps 20 [--q8 | --q6k]
+    python -m fak_amd.q4kbench --n 3584 --k 18944 --floor records|read
 
 Weights rotate over enough distinct device copies (> 256 MB) that the Infinity Cache cannot
-serve them.
+serve them. --floor times a launch that only moves the Q4_K weight's bytes, with no arithmetic:
+`records` in the one-token GEMV's own grid and record loads (fhip_probe_q4k_records), `read` as
+a plain grid-stride read of the same bytes (fhip_probe_read).
 """
 from __future__ import annotations
 
@@ -25,6 +28,8 @@ def main() -> None:
     ap.add_argument("--q8", action="store_true", help="Q8_0 weights instead of Q4_K")
     ap.add_argument("--q6k", action="store_true", help="Q6_K weights instead of Q4_K")
     ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--floor", choices=("records", "read"), default=None,
+                    help="time a no-arithmetic pass over the Q4_K weight instead of the matmul")
     a = ap.parse_args()
     fakhip.init()
     lib = fakhip.load()
@@ -58,21 +63,37 @@ def main() -> None:
     e0, e1 = C.c_void_p(), C.c_void_p()
     fakhip.call("fhip_event_create", C.byref(e0))
     fakhip.call("fhip_event_create", C.byref(e1))
-    fakhip.call(mm, ptrs[0], dx, dy, a.n, a.k, a.m)
+    if a.floor:
+        if a.q8 or a.q6k:
+            raise SystemExit("--floor measures a Q4_K weight")
+        if a.floor == "records":
+            words = lib.fhip_probe_q4k_records_sink_words(a.n, a.k)
+            sink = fakhip.alloc_call("fhip_malloc", 4 * words)
+            run = lambda p: fakhip.call("fhip_probe_q4k_records", p, a.n, a.k, sink)
+        else:
+            words = lib.fhip_probe_read_sink_words(nbytes)
+            sink = fakhip.alloc_call("fhip_malloc", 4 * words)
+            run = lambda p: fakhip.call("fhip_probe_read", p, nbytes, sink)
+    else:
+        sink = None
+        run = lambda p: fakhip.call(mm, p, dx, dy, a.n, a.k, a.m)
+    run(ptrs[0])
     fakhip.call("fhip_sync")
     fakhip.call("fhip_event_record", e0)
     for i in range(a.reps):
-        fakhip.call(mm, ptrs[i % len(ptrs)], dx, dy, a.n, a.k, a.m)
+        run(ptrs[i % len(ptrs)])
     fakhip.call("fhip_event_record", e1)
     ms = C.c_float()
     fakhip.call("fhip_event_elapsed_ms", e0, e1, C.byref(ms))
     us = ms.value * 1e3 / a.reps
-    bytes_ = alg + 4 * a.m * (a.n + a.k)
-    print(json.dumps({"n": a.n, "k": a.k, "m": a.m, "q8_0": a.q8, "q6_k": a.q6k, "reps": a.reps,
+    # a floor moves the packed weight only; the matmul counts its activations and outputs too
+    bytes_ = nbytes if a.floor else alg + 4 * a.m * (a.n + a.k)
+    print(json.dumps({"n": a.n, "k": a.k, "m": a.m, "q8_0": a.q8, "q6_k": a.q6k,
+                      "floor": a.floor, "reps": a.reps,
                       "us_per_call": round(us, 3), "GBs": round(bytes_ / us / 1e3, 1),
                       "TFLOPs": round(2.0 * a.m * a.n * a.k / us / 1e6, 2),
                       "weight_copies": len(ptrs)}), flush=True)
-    for p in ptrs + [dx, dy]:
+    for p in ptrs + [dx, dy] + ([sink] if sink else []):
         lib.fhip_free(p)
 
 

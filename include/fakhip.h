@@ -110,6 +110,11 @@ int fhip_event_destroy(void *event);
 int fhip_event_record(void *event);
 /* Wait for `end`, then report the elapsed milliseconds between two recorded events. */
 int fhip_event_elapsed_ms(void *start, void *end, float *ms);
+/* Measurement hook (no counterpart in the reference): the next 1..4-token Q4_K GEMV launch
+ * records `start` and `stop` at its own dispatch's start and end (hipExtLaunchKernel), so
+ * fhip_event_elapsed_ms gives that kernel's duration without queue or host time. Refused
+ * during graph capture; captured launches leave a pending pair for the next eager one. */
+int fhip_time_next_launch(void *start, void *stop);
 
 /* ---- Q4_K (256-weight super-blocks of 144 B: f16 d, f16 dmin, 12 B of 6-bit scales/mins,
  *      128 B of nibbles; internal/model/quant_q4k.go:22-26) ------------------------------- */
@@ -170,6 +175,19 @@ int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, float *dY, in
  * it. */
 int fhip_q4k_matmul_noalloc_f32(const void *dPacked, const float *dX, float *dY, int out, int in,
                                 int P);
+
+/* Measurement hooks for the decode GEMV's bandwidth floors (no counterpart in the reference;
+ * for profiling this backend). Each folds what it reads into one word per wave, written to
+ * dSink (a device buffer of the *_sink_words count of uint32), so no load is dropped.
+ * fhip_probe_read: every byte of d read once (16-byte non-temporal loads, a contiguous 16 KB per
+ * workgroup, four per thread all issued before any is used): the plain-read ceiling of one
+ * launch.
+ * fhip_probe_q4k_records: the one-token GEMV's own grid and record loads over a tiled Q4_K
+ * weight, with no arithmetic. */
+size_t fhip_probe_read_sink_words(size_t bytes);
+int fhip_probe_read(const void *d, size_t bytes, uint32_t *dSink);
+size_t fhip_probe_q4k_records_sink_words(int out, int in);
+int fhip_probe_q4k_records(const void *dPacked, int out, int in, uint32_t *dSink);
 
 /* ---- Q6_K (256-weight super-blocks of 210 B; internal/model/quant_kquant.go:45,139-163) ---- */
 

@@ -99,3 +99,37 @@ def test_captured_stream_workspace_freed_after_graph(weight):
         print(f"[runtime] free before {before / MiB:.0f} MiB, after graph + stream "
               f"{after / MiB:.0f} MiB", flush=True)
         assert after >= before - 8 * MiB
+
+
+def test_time_next_launch_stamps_one_dispatch(weight):
+    """fhip_time_next_launch's events are stamped by the next one-token GEMV dispatch only: its
+    duration is positive and below the launch-to-sync wall time of the same call, and a second
+    call leaves the pair as it was."""
+    import time
+    lib = fakhip.load()
+    X = synth.activations(1, IN, 94)
+    ev = [C.c_void_p(), C.c_void_p()]
+    for e in ev:
+        fakhip.call("fhip_event_create", C.byref(e))
+    try:
+        with Dev.from_host(X) as dx, Dev(OUT * 4) as dy:
+            fakhip.call("fhip_q4k_matmul_f32", weight, dx.ptr, dy.ptr, OUT, IN, 1)
+            fakhip.call("fhip_sync")
+            fakhip.call("fhip_time_next_launch", ev[0], ev[1])
+            t0 = time.perf_counter()
+            fakhip.call("fhip_q4k_matmul_f32", weight, dx.ptr, dy.ptr, OUT, IN, 1)
+            fakhip.call("fhip_sync")
+            wall_ms = 1e3 * (time.perf_counter() - t0)
+            ms = C.c_float()
+            fakhip.call("fhip_event_elapsed_ms", ev[0], ev[1], C.byref(ms))
+            first = ms.value
+            print(f"[runtime] dispatch {first * 1e3:.2f} us, wall {wall_ms * 1e3:.1f} us", flush=True)
+            assert 0.0 < first < wall_ms
+            fakhip.call("fhip_q4k_matmul_f32", weight, dx.ptr, dy.ptr, OUT, IN, 1)
+            fakhip.call("fhip_sync")
+            fakhip.call("fhip_event_elapsed_ms", ev[0], ev[1], C.byref(ms))
+            assert ms.value == first
+        assert lib.fhip_time_next_launch(None, ev[1]) == fakhip.EINVAL
+    finally:
+        for e in ev:
+            fakhip.call("fhip_event_destroy", e)
