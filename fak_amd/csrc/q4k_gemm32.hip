@@ -503,12 +503,23 @@ constexpr int wait_vm(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }  /
 // (256 VGPRs, two per SIMD) measured slower at every size (M=512 112.7 against 106.5 us, M=2048
 // 413 against 376, with the records still in LDS) and no longer fit their registers.
 constexpr int kGemmWaves = 4;
-__global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu(3, 3))) void q4k_gemm32s_kernel(
+// Loads a wave may leave pending at the end of stage ls (0..7) of a super-block: the DMA of the
+// two later stages (kdma each), and for Q6_K the record group issued at stage 0 (6 loads)
+// through stage 2 and the one issued at stage 4 (8 loads) through stage 6. Q4_K's records (2
+// and 3 loads) complete within the stage after their issue: with plain loads pending beside
+// the LDS DMA the compiler no longer trusts the counter's order and drains it (vmcnt(0)) before
+// the next read of a DMA buffer, twice per super-block, which measured the same.
+constexpr int gemm32s_wait(int fmt, int ls, int kdma) {
+  return fmt == 0 ? 2 * kdma
+                  : 2 * kdma + (ls <= 2 ? 6 : 0) + (ls >= 4 && ls <= 6 ? 8 : 0);
+}
+template <int FMT, int WPE>
+__global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void quant_gemm32s_kernel(
     const uint8_t *__restrict__ W, const uint4 *__restrict__ xa,
     const float *__restrict__ tscale, float *__restrict__ Y, int N,
     int M, int nblk, int ntiles, int MTG, int F, int S, int R, float *__restrict__ part) {
   constexpr int NW = kGemmWaves;
-  constexpr int kUnits = kQ4kRecord / 16;                       // 144 units per record
+  constexpr int kUnits = kQ4kRecord / 16;                       // 144 units per Q4_K record
   constexpr int kSU = 4 * 2 * 64;                               // 512 units (8 KB) per stage
   constexpr int NT = 4 / NW;                                    // 32-row MFMA tiles per wave
   constexpr int kDMA = 8 / NW;                                  // stage loads per wave
@@ -549,32 +560,64 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
   };
   auto buf = [&](int k) -> u32x4 * { return k == 0 ? As0 : k == 1 ? As1 : k == 2 ? As2 : As3; };
 
-  // The weights go straight to registers: lane (kap, rho) needs, per super-block and 32-row tile
-  // t, the 16 header bytes of row rho % 16 of 16-row tile tl(t) and four 16-byte units of nibble
-  // bytes (lane group 2 h + kap of chunks 2 c2, 2 c2 + 1). Rows past N read the last tile.
+  // The weights go straight to registers. Q4_K: lane (kap, rho) needs, per super-block and
+  // 32-row tile t, the 16 header bytes of row rho % 16 of 16-row tile tl(t) and four 16-byte
+  // units of nibble bytes (lane group 2 h + kap of chunks 2 c2, 2 c2 + 1). Q6_K: the row's 16
+  // int8 scales and f16 d, and per half hh of the super-block (chunks 2 hh, 2 hh + 1) the lane's
+  // 8 ql bytes of each of the four groups and 8 qh bytes of each K16 half. Rows past N read the
+  // last tile.
   auto tl = [&](int t) { return (8 / NW) * wave + 2 * t + (rho >> 4); };
   const int r16 = rho & 15;
   const u32x4 *Wv = reinterpret_cast<const u32x4 *>(W);
   auto rec = [&](int t, int b) {
     return Wv + ((size_t)min(tile0 + tl(t), ntiles - 1) * nblk + b) * kUnits;
   };
+  auto rec6 = [&](int t, int b) {
+    return W + ((size_t)min(tile0 + tl(t), ntiles - 1) * nblk + b) * kQ6kRecord;
+  };
   auto nib = [&](int c2, int h) { return kQ4kHdr / 16 + 64 * c2 + 16 * (2 * h + kap) + r16; };
-  u32x4 hdr[NT], u0[NT][2], u1[NT][2];
+  u32x4 hdr[NT], u0[NT][2], u1[NT][2];    // Q4_K
+  uint2 ql6[NT][2][4], qh6[NT][2][2];     // Q6_K: [half][group], [half][K16 half]
+  uint32_t dw6[NT];                       // Q6_K: the row's d (f16 bits)
   auto load_hu0 = [&](int b) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const u32x4 *r = rec(t, b);
-      hdr[t] = r[r16];
-      u0[t][0] = r[nib(0, 0)];
-      u0[t][1] = r[nib(0, 1)];
+      if (FMT == 0) {
+        const u32x4 *r = rec(t, b);
+        hdr[t] = r[r16];
+        u0[t][0] = r[nib(0, 0)];
+        u0[t][1] = r[nib(0, 1)];
+      } else {
+        const uint8_t *r = rec6(t, b);
+        hdr[t] = *reinterpret_cast<const u32x4 *>(r + 16 * r16);
+        dw6[t] = *reinterpret_cast<const uint16_t *>(r + kQ6kD + 2 * r16);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          ql6[t][0][g] = *reinterpret_cast<const uint2 *>(r + kQ6kQl + 16 * (16 * g + r16) + 8 * kap);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          qh6[t][0][h] = *reinterpret_cast<const uint2 *>(r + kQ6kQh + 256 * h + 16 * r16 + 8 * kap);
+      }
     }
   };
   auto load_u1 = [&](int b) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const u32x4 *r = rec(t, b);
-      u1[t][0] = r[nib(1, 0)];
-      u1[t][1] = r[nib(1, 1)];
+      if (FMT == 0) {
+        const u32x4 *r = rec(t, b);
+        u1[t][0] = r[nib(1, 0)];
+        u1[t][1] = r[nib(1, 1)];
+      } else {
+        const uint8_t *r = rec6(t, b);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          ql6[t][1][g] = *reinterpret_cast<const uint2 *>(r + kQ6kQl + 1024 + 16 * (16 * g + r16) +
+                                                          8 * kap);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          qh6[t][1][h] = *reinterpret_cast<const uint2 *>(r + kQ6kQh + 512 + 256 * h + 16 * r16 +
+                                                          8 * kap);
+      }
     }
   };
 
@@ -600,28 +643,48 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
   // it: the compiler would otherwise hoist the dequantization next to the load and wait for it
   // there (vmcnt(0)), with the registers of both held at once.
   auto pin = [](u32x4 &v) { asm volatile("" : "+v"(v)); };
+  auto pin2 = [](uint2 &v) { asm volatile("" : "+v"(v.x), "+v"(v.y)); };
   for (int b = kb0; b < kb1; ++b) {
     RowScales rs[NT];
+    uint32_t sc6[NT][4];  // Q6_K: the row's 16 int8 scales, one word per chunk
+    float d6[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       pin(hdr[t]);
-      rs[t] = row_scales(__builtin_bit_cast(uint4, hdr[t]), K);
+      if (FMT == 0) {
+        rs[t] = row_scales(__builtin_bit_cast(uint4, hdr[t]), K);
+      } else {
+        asm volatile("" : "+v"(dw6[t]));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc6[t][j] = hdr[t][j];
+        d6[t] = (float)__builtin_bit_cast(_Float16, (uint16_t)dw6[t]);
+      }
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       if (c == 0 || c == 2)
 #pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          if (FMT == 0) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) pin(c == 0 ? u0[t][h] : u1[t][h]);
+          } else {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) pin2(ql6[t][c >> 1][g]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) pin2(qh6[t][c >> 1][h]);
+          }
+        }
+      uint2 xb[NT][2];  // Q4_K: nibble bytes of lane group g = 2 h + kap of chunk c
+      if (FMT == 0) {
+#pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-          for (int h = 0; h < 2; ++h) pin(c == 0 ? u0[t][h] : u1[t][h]);
-      uint2 xb[NT][2];  // nibble bytes of lane group g = 2 h + kap of chunk c, every row tile
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const u32x4 v = c < 2 ? u0[t][h] : u1[t][h];
-          xb[t][h] = (c & 1) ? make_uint2(v[2], v[3]) : make_uint2(v[0], v[1]);
-        }
+          for (int h = 0; h < 2; ++h) {
+            const u32x4 v = c < 2 ? u0[t][h] : u1[t][h];
+            xb[t][h] = (c & 1) ? make_uint2(v[2], v[3]) : make_uint2(v[0], v[1]);
+          }
+      }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int ls = 2 * c + h;  // stage within the super-block (its buffer is ls & 3)
@@ -635,7 +698,19 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
         const u32x4 *Acur = buf(ls & 3);
         f16x8 bl[NT], bh[NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) dequant8(xb[t][h].x, xb[t][h].y, rs[t], c, K, bl[t], bh[t]);
+        for (int t = 0; t < NT; ++t) {
+          if (FMT == 0) {
+            dequant8(xb[t][h].x, xb[t][h].y, rs[t], c, K, bl[t], bh[t]);
+          } else {
+            // K16 slices h (ql group h) and 2 + h (group 2 + h) of chunk c: nibble c & 1 of the
+            // half's ql bytes, 2-bit fields of its qh bytes; scales of sub-blocks 4c + h, 4c + 2 + h
+            const uint32_t scw = sc6[t][c];
+            const _Float16 Sa = (_Float16)(d6[t] * (float)(int8_t)(scw >> (8 * h)));
+            const _Float16 Sb = (_Float16)(d6[t] * (float)(int8_t)(scw >> (8 * (2 + h))));
+            dequant6(ql6[t][c >> 1][h], ql6[t][c >> 1][2 + h], qh6[t][c >> 1][h], c & 1, Sa, Sb,
+                     in_reg(0x0F0F0F0Fu), in_reg(0x03030303u), K, bl[t], bh[t]);
+          }
+        }
 #pragma unroll
         for (int hi = 0; hi < 2; ++hi) {
 #pragma unroll
@@ -647,11 +722,18 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
           }
         }
         // Stage s + 1 has landed (for every wave, after the barrier) once at most stages s + 2
-        // and s + 3 (kDMA loads each) are pending. The record loads of this stage complete by
-        // then too: with plain loads still pending beside the LDS DMA the compiler no longer
-        // trusts the counter's order and waits for all loads (vmcnt(0)) before the next stage's
-        // operand reads; letting them stay in flight that way measured no faster.
-        FHIP_LDS_BARRIER(wait_vm(2 * kDMA));
+        // and s + 3 (kDMA loads each) and the record loads that gemm32s_wait allows are
+        // pending.
+        switch (ls) {
+          case 0: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 0, kDMA))); break;
+          case 1: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 1, kDMA))); break;
+          case 2: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 2, kDMA))); break;
+          case 3: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 3, kDMA))); break;
+          case 4: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 4, kDMA))); break;
+          case 5: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 5, kDMA))); break;
+          case 6: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 6, kDMA))); break;
+          default: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 7, kDMA))); break;
+        }
       }
     }
   }
@@ -739,7 +821,7 @@ GemmPlan plan_gemm32(int fmt, int N, int K, int M) {
   // FAK_HIP_GEMM32_FORM=1: the four-wave 2x2 kernel (a comparison; it agrees bit for bit with
   // the default without a K split). Default: the staged kernel, measured faster from 64 to 2048
   // tokens.
-  p.form = fmt == 0 ? tuning().gemm32_form : 1;
+  p.form = tuning().gemm32_form;
   p.F = p.tasks;
   p.S = 1;
   p.R = 0;
@@ -805,6 +887,12 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
     return FHIP_OK;
   };
   const int grid2 = p.F + p.R * p.S;
+  if (fmt == 1 && p.form != 1) {
+    quant_gemm32s_kernel<1, 2><<<grid2, 64 * kGemmWaves, 0, stream()>>>(
+        W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
+    FHIP_CHECK_LAUNCH("quant_gemm32s_kernel<1>");
+    return reduce();
+  }
   if (fmt == 1) {  // 60 KB of LDS with one weight buffer: two workgroups per CU
     quant_gemm32_kernel<1, 1, 2><<<grid2, 256, 0, stream()>>>(W, xa, ts, Y, N, M, nblk, ntiles,
                                                                MTG, p.F, p.S, p.R, part);
@@ -812,9 +900,9 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
     return reduce();
   }
   if (p.form != 1) {
-    q4k_gemm32s_kernel<<<grid2, 64 * kGemmWaves, 0, stream()>>>(
+    quant_gemm32s_kernel<0, 3><<<grid2, 64 * kGemmWaves, 0, stream()>>>(
         W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
-    FHIP_CHECK_LAUNCH("q4k_gemm32s_kernel");
+    FHIP_CHECK_LAUNCH("quant_gemm32s_kernel<0>");
     return reduce();
   }
   if (tuning().gemm32_nwb == 2)

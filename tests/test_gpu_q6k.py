@@ -7,7 +7,7 @@ import pytest
 
 from fak_amd import fakhip
 from tests import q6k_cases as qc
-from tests.gpu_util import Dev, rel_err
+from tests.gpu_util import Dev, knobs, rel_err, spread_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -126,9 +126,33 @@ def test_gemm_prefill_matches_oracle(hip, oracle_mod, out, in_, P, rows):
         ref, got = oracle_mod.q6k_gemm(raw, out, in_, X, P), Y
     else:
         rb = (in_ // 256) * 210
-        sel = np.concatenate([np.arange(rows // 2), np.arange(out - rows // 2, out)])
+        sel = spread_rows(out, per_block=max(1, rows // max(1, out // 128)))
         sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
         ref, got = oracle_mod.q6k_gemm(sub, len(sel), in_, X, P), Y[:, sel]
     err = rel_err(got, ref)
+    print(f"    max|d|/RMS = {err:.2e}", flush=True)
+    assert err <= 1e-2
+
+
+@pytest.mark.parametrize("out,in_,P", [(300, 768, 40), (1000, 2048, 200), (152, 4096, 131),
+                                       (3584, 18944, 128), (18944, 3584, 512)])
+def test_gemm_forms_bit_identical(hip, oracle_mod, monkeypatch, out, in_, P):
+    """The staged prefill GEMM (the default: weights loaded straight to the registers of the
+    lanes that use them) and the four-wave 2x2 form (records staged through LDS) share the tile,
+    the K order, the dequantized f16 weights and each accumulator's MFMA sequence: on Q6_K their
+    outputs agree bit for bit (ragged row and token tiles, K-split and whole tiles), and the
+    staged result meets the GEMM bound against the oracle on rows spread over every row tile."""
+    print(f"[case] q6k gemm forms out={out} in={in_} P={P}", flush=True)
+    rng = np.random.default_rng(out + 3 * P)
+    raw = qc.pin_d(rng.integers(0, 256, size=out * (in_ // 256) * 210, dtype=np.uint8), 0x1400)
+    X = rng.standard_normal((P, in_)).astype(np.float32)
+    with knobs(monkeypatch, FAK_HIP_GEMM32_FORM=1):
+        Y1 = dev_matmul(raw, out, in_, X, P)
+    Y2 = dev_matmul(raw, out, in_, X, P)
+    assert np.array_equal(Y1.view(np.uint32), Y2.view(np.uint32))
+    rb = (in_ // 256) * 210
+    sel = spread_rows(out, per_block=1) if out > 1024 else np.arange(out)
+    sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
+    err = rel_err(Y2[:, sel], oracle_mod.q6k_gemm(sub, len(sel), in_, X, P))
     print(f"    max|d|/RMS = {err:.2e}", flush=True)
     assert err <= 1e-2
