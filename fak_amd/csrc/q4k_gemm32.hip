@@ -788,13 +788,19 @@ __global__ __launch_bounds__(256) void gemm32_reduce_kernel(const float *__restr
   // Range s (1 .. S-1) of this tile's quad: part + ((s - 1) R + r) kQuads + e4.
   const float4 *pp = reinterpret_cast<const float4 *>(part) + (size_t)r * kQuads + e4;
   float *y = Y + (size_t)tok * N + o0;
+  const size_t stride = (size_t)R * kQuads;
+  if ((N & 3) == 0 && ((uintptr_t)Y & 15) == 0) {
+    // the quad is 16-byte aligned and whole: one load and one store of Y
+    float4 *y4 = reinterpret_cast<float4 *>(y);
+    *y4 = add_ranges(*y4, pp, stride, S - 1);
+    return;
+  }
   const int nv = min(4, N - o0);
   float4 v0;
   v0.x = y[0];
   v0.y = nv > 1 ? y[1] : 0.f;
   v0.z = nv > 2 ? y[2] : 0.f;
   v0.w = nv > 3 ? y[3] : 0.f;
-  const size_t stride = (size_t)R * kQuads;
   const float4 v = add_ranges(v0, pp, stride, S - 1);
   y[0] = v.x;
   if (nv > 1) y[1] = v.y;
