@@ -2,7 +2,7 @@
 tokens, a number of repetitions, median-free plain timing with HIP events, and a one-line report.
 Used as the target program for rocprofv3 runs (kernel trace, counters) on one shape.
 
-    python -m fak_amd.q4kbench --n 18944 --k 3584 --m 1 --reps 20 [--q8 | --q6k]
+    python -m fak_amd.q4kbench --n 18944 --k 3584 --m 1 --reps 20 [--q8 | --q6k | --int8]
     python -m fak_amd.q4kbench --n 3584 --k 18944 --floor records|read
 
 Weights rotate over enough distinct device copies (> 256 MB) that the Infinity Cache cannot
@@ -27,6 +27,8 @@ def main() -> None:
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--q8", action="store_true", help="Q8_0 weights instead of Q4_K")
     ap.add_argument("--q6k", action="store_true", help="Q6_K weights instead of Q4_K")
+    ap.add_argument("--int8", action="store_true",
+                    help="the int8 Q4_K route (fhip_q4k_matmul_int8_f32) instead of the f32 one")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--floor", choices=("records", "read"), default=None,
                     help="time a no-arithmetic pass over the Q4_K weight instead of the matmul")
@@ -49,6 +51,8 @@ def main() -> None:
     else:
         raw = synth.q4k_weights(a.n, a.k, a.seed)
         up, mm, nbytes = "fhip_q4k_upload", "fhip_q4k_matmul_f32", lib.fhip_q4k_packed_bytes(a.n, a.k)
+        if a.int8:
+            mm = "fhip_q4k_matmul_int8_f32"
         alg = a.n * (a.k // 256) * 144
     p0 = fakhip.alloc_call(up, raw.ctypes.data, a.n, a.k)
     ptrs = [p0]
@@ -89,7 +93,7 @@ def main() -> None:
     # a floor moves the packed weight only; the matmul counts its activations and outputs too
     bytes_ = nbytes if a.floor else alg + 4 * a.m * (a.n + a.k)
     print(json.dumps({"n": a.n, "k": a.k, "m": a.m, "q8_0": a.q8, "q6_k": a.q6k,
-                      "floor": a.floor, "reps": a.reps,
+                      "floor": a.floor, "int8": a.int8, "reps": a.reps,
                       "us_per_call": round(us, 3), "GBs": round(bytes_ / us / 1e3, 1),
                       "TFLOPs": round(2.0 * a.m * a.n * a.k / us / 1e6, 2),
                       "weight_copies": len(ptrs)}), flush=True)
