@@ -303,12 +303,9 @@ __device__ __forceinline__ float silu_f32(float z) {
 // Weight records each wave keeps in flight (LDS path) and the widest workgroup (waves) for one
 // token. Measured at the 7B FFN shapes: an 8-record ring with 8-wave workgroups, the
 // activation loads issued ahead of the ring, and lane-parallel coalesced quantization were all
-// slower (11.9-12 us gate/up, 14.7-15.1 us down, against 10.6 and 13.8 us here).
-
-// Weight records each wave keeps in flight (LDS path) and the widest workgroup (waves) for one
-// token. Measured at the 7B FFN shapes: an 8-record ring with 8-wave workgroups, the
-// activation loads issued ahead of the ring, and lane-parallel coalesced quantization were all
-// slower (11.9-12 us gate/up, 14.7-15.1 us down, against 10.6 and 13.8 us here).
+// slower (11.9-12 us gate/up, 14.7-15.1 us down, against 10.6 and 13.8 us here); so were rings
+// of 5 and 6 records with the present workgroups (gate/up 10.1 / 10.3 against 9.6 us, down
+// 11.4 / 11.8-12.2 against 11.3), though every down wave then holds all its records at once.
 constexpr int kPF1 = 4, kMaxWaves1 = 16;
 // Most super-blocks (of all tokens) a wave quantizes from activations loaded before its records.
 constexpr int kXPre = 8;
