@@ -328,15 +328,18 @@ extern "C" int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, fl
     FHIP_CHECK_LAUNCH("i8r_prep_kernel");
   }
   // Shape: a 16-row tile per workgroup whose records are split over up to 8 waves until the grid
-  // has ~16 waves per CU (each wave keeping >= 2 records); a window of records whose LDS fits
-  // the device.
+  // has ~16 waves per CU (~8 for one token), each wave keeping >= 2 records; a window of records
+  // whose LDS fits the device. (One token with ~16 waves per CU put 4 waves on each 18944 x 3584
+  // tile: 26.2 us against 21.4 with 2; the 3584 x 18944 down projection keeps 8 either way.
+  // Eight tokens on 18944 x 3584 want 4: 91 us, 130 with 2.)
   const int ntiles = q4k_tiles(out);
   const int groups = ceil_div(P, kTokGroup);
   const int pg = P < kTokGroup ? P : kTokGroup;
   int KW = tuning().i8r_kw;
   if (KW <= 0) {
     KW = 1;
-    while (KW < 8 && (long long)ntiles * groups * KW < 16LL * cu_count() && nblk >= 2 * KW)
+    const long long fill = (P == 1 ? 8LL : 16LL) * cu_count();
+    while (KW < 8 && (long long)ntiles * groups * KW < fill && nblk >= 2 * KW)
       KW *= 2;
   }
   if (KW > 8) KW = 8;
