@@ -704,10 +704,14 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
           } else {
             // K16 slices h (ql group h) and 2 + h (group 2 + h) of chunk c: nibble c & 1 of the
             // half's ql bytes, 2-bit fields of its qh bytes; scales of sub-blocks 4c + h, 4c + 2 + h
-            const uint32_t scw = sc6[t][c];
-            const _Float16 Sa = (_Float16)(d6[t] * (float)(int8_t)(scw >> (8 * h)));
-            const _Float16 Sb = (_Float16)(d6[t] * (float)(int8_t)(scw >> (8 * (2 + h))));
-            dequant6(ql6[t][c >> 1][h], ql6[t][c >> 1][2 + h], qh6[t][c >> 1][h], c & 1, Sa, Sb,
+            uint32_t scw = sc6[t][c];
+            float dd6 = d6[t];
+            uint2 qa = ql6[t][c >> 1][h], qb = ql6[t][c >> 1][2 + h], qhh = qh6[t][c >> 1][h];
+            pin2(qa); pin2(qb); pin2(qhh);
+            asm volatile("" : "+v"(scw), "+v"(dd6));
+            const _Float16 Sa = (_Float16)(dd6 * (float)(int8_t)(scw >> (8 * h)));
+            const _Float16 Sb = (_Float16)(dd6 * (float)(int8_t)(scw >> (8 * (2 + h))));
+            dequant6(qa, qb, qhh, c & 1, Sa, Sb,
                      in_reg(0x0F0F0F0Fu), in_reg(0x03030303u), K, bl[t], bh[t]);
           }
         }
@@ -720,6 +724,10 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
             for (int t = 0; t < NT; ++t)
               acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, hi ? bh[t] : bl[t], acc[i][t], 0, 0, 0);
           }
+          // Q6_K: the second K16 half's operand reads wait for the first half's MFMAs, and each
+          // stage's code words enter through fresh pinned copies: so scheduled the kernel needs
+          // 145 VGPRs and runs three workgroups per CU (219, and two, before).
+          if (FMT == 1 && hi == 0) __builtin_amdgcn_sched_barrier(0);
         }
         // Stage s + 1 has landed (for every wave, after the barrier) once at most stages s + 2
         // and s + 3 (kDMA loads each) and the record loads that gemm32s_wait allows are
@@ -894,7 +902,7 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
   };
   const int grid2 = p.F + p.R * p.S;
   if (fmt == 1 && p.form != 1) {
-    quant_gemm32s_kernel<1, 2><<<grid2, 64 * kGemmWaves, 0, stream()>>>(
+    quant_gemm32s_kernel<1, 3><<<grid2, 64 * kGemmWaves, 0, stream()>>>(
         W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
     FHIP_CHECK_LAUNCH("quant_gemm32s_kernel<1>");
     return reduce();
