@@ -144,12 +144,14 @@ struct GemmFmt {
 // One workgroup per (padded) token: a max-reduce over the row, then the conversion. UPT > 0: each
 // thread loads its UPT 8-value units of the row at once (unconditionally, indices clamped to the
 // row; a repeated unit changes neither the maximum nor the NaN flag) and converts them from its
-// registers, so the row is read once with every load in flight together (rows of K <= 2048 UPT).
+// registers, so the row is read once with every load in flight together (rows of K <= 8 NT UPT).
 // UPT = 0: a loop over the row, read twice (the second pass hits L2), for longer rows.
-constexpr int kXprepThreads = 256;
-template <int UPT>
-__global__ __launch_bounds__(kXprepThreads) void gemm32_xprep_kernel(
+// NT: threads per workgroup, 256, or 1024 for rows longer than 8192 values, so that each thread
+// holds fewer of them (K=18944 at M=512: 15.1 us against 16.2 with 256 threads of 12 units).
+template <int UPT, int NT>
+__global__ __launch_bounds__(NT) void gemm32_xprep_kernel(
     const float *__restrict__ X, int M, int K, uint4 *__restrict__ xa, float *__restrict__ tscale) {
+  constexpr int kXprepThreads = NT;
   __shared__ float wmax[kXprepThreads / 64];
   // Token of this workgroup: the 32 tokens of an operand tile run on one XCD (workgroups go to
   // the 8 XCDs round-robin), so one L2 assembles each 512-byte operand block from its 32 16-byte
@@ -230,22 +232,29 @@ __global__ __launch_bounds__(kXprepThreads) void gemm32_xprep_kernel(
   }
 }
 
-// Launches the activation prep with the smallest register-resident unit count that covers K.
+// Launches the activation prep with the smallest register-resident unit count that covers K:
+// 256 threads per token up to 8192 values, 1024 above.
 void launch_xprep(const float *X, int M, int K, int MTG, uint4 *xa, float *ts) {
-  const int upt = ceil_div(K / 8, kXprepThreads);
   const unsigned grid = MTG * kBM;
-  if (upt <= 2)
-    gemm32_xprep_kernel<2><<<grid, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
+  if (K <= 8192) {
+    const int upt = ceil_div(K / 8, 256);
+    if (upt <= 2)
+      gemm32_xprep_kernel<2, 256><<<grid, 256, 0, stream()>>>(X, M, K, xa, ts);
+    else
+      gemm32_xprep_kernel<4, 256><<<grid, 256, 0, stream()>>>(X, M, K, xa, ts);
+    return;
+  }
+  const int upt = ceil_div(K / 8, 1024);
+  if (upt <= 1)
+    gemm32_xprep_kernel<1, 1024><<<grid, 1024, 0, stream()>>>(X, M, K, xa, ts);
+  else if (upt <= 2)
+    gemm32_xprep_kernel<2, 1024><<<grid, 1024, 0, stream()>>>(X, M, K, xa, ts);
+  else if (upt <= 3)
+    gemm32_xprep_kernel<3, 1024><<<grid, 1024, 0, stream()>>>(X, M, K, xa, ts);
   else if (upt <= 4)
-    gemm32_xprep_kernel<4><<<grid, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
-  else if (upt <= 8)
-    gemm32_xprep_kernel<8><<<grid, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
-  else if (upt <= 12)
-    gemm32_xprep_kernel<12><<<grid, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
-  else if (upt <= 16)
-    gemm32_xprep_kernel<16><<<grid, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
+    gemm32_xprep_kernel<4, 1024><<<grid, 1024, 0, stream()>>>(X, M, K, xa, ts);
   else
-    gemm32_xprep_kernel<0><<<grid, kXprepThreads, 0, stream()>>>(X, M, K, xa, ts);
+    gemm32_xprep_kernel<0, 1024><<<grid, 1024, 0, stream()>>>(X, M, K, xa, ts);
 }
 
 // FMT: 0 Q4_K, 1 Q6_K. NWB: LDS buffers for the weight records (2: the next super-block loads
