@@ -66,6 +66,7 @@ struct Tuning {
   int gemm32_sk;          // FAK_HIP_GEMM32_SK: K ranges of the prefill GEMM
   int gemm32_nwb;         // FAK_HIP_GEMM32_NWB: weight buffers of the 2x2 form (1 or 2)
   int i8r_kw;             // FAK_HIP_I8R_KW: waves per tile of the int8 route
+  int i8r_tw;             // FAK_HIP_I8R_TW: tiles per workgroup of the int8 route (one wave each)
   int q8_tw, q8_kw;       // FAK_HIP_Q8_TW / _KW: Q8_0 GEMV workgroup shape
 };
 const Tuning &tuning();

@@ -11,8 +11,9 @@
 // Every float operation is a single IEEE-rounded operation, so this file is built with
 // -ffp-contract=off and the only freedom is in the integer sums.
 //
-// Device plan. A workgroup owns one 16-row tile (tiled.hpp) and a group of up to 16 tokens, its
-// KW waves each taking a contiguous part of the super-blocks of a window of records.
+// Device plan. A workgroup owns TW 16-row tiles (tiled.hpp) and a group of up to 16 tokens: one
+// tile whose KW waves each take a contiguous part of the super-blocks of a window of records,
+// or (KW = 1) TW tiles of one wave each, which share the workgroup's staged activations.
 //   * staging: the workgroup quantizes the window's activation blocks exactly as the reference
 //     does (q8round.hpp) into LDS: int8 codes and per block {f32(S), dx}. The first weight
 //     records of every wave are already in flight meanwhile.
@@ -22,10 +23,10 @@
 //     pieces and the codes of token r at the same positions; result lane (g, r) holds I_s of
 //     row r for tokens 4g..4g+3 and forms the two terms T1 = (f32(I) * ws) * dx and
 //     T2 = (f32(S) * wm) * dx with the reference's roundings.
-//   * the chain: wave 0's lanes own the (row, token) sums. Wave 0 adds the terms of its own
-//     part as it makes them; the other waves park theirs in LDS and wave 0 adds them after a
-//     barrier, in record order. A window's terms must fit in LDS; long rows or many tokens take
-//     several windows, the sums carrying across.
+//   * the chain: a tile's first wave owns its (row, token) sums and adds the terms of its own
+//     part as it makes them; with KW > 1 the other waves park theirs in LDS and the first wave
+//     adds them after a barrier, in record order. A window's terms must fit in LDS; long rows or
+//     many tokens take several windows, the sums carrying across.
 // Weight records stream through a ring of PF in-flight loads per wave (three 16-byte loads per
 // lane per record), as in the Q4_K GEMV.
 #include "kernels.hpp"
@@ -110,19 +111,23 @@ template <int NV>
 __global__ __launch_bounds__(512) void q4k_i8route_kernel(
     const uint8_t *__restrict__ W, const float *__restrict__ X, const int8_t *__restrict__ qxg,
     const float2 *__restrict__ sdg, float *__restrict__ Y, int N, int K, int nblk, int P,
-    int Wrec, int KW, int fused) {
+    int Wrec, int KW, int TW, int fused) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const int tile = blockIdx.x;
   const int t0 = blockIdx.y * kTokGroup;
   const int pg = min(kTokGroup, P - t0);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // This wave's tile and its part of the tile's records (TW > 1 only with KW = 1). A wave whose
+  // tile is past the matrix streams the last tile and writes nothing.
+  const int ntiles = (N + 15) / 16;
+  const int tile = blockIdx.x * TW + wave / KW, kwave = wave - (wave / KW) * KW;
+  const int gtile = min(tile, ntiles - 1);
   const int g = lane >> 4, r = lane & 15;
   const I8rLds L = i8r_lds(pg, Wrec, KW);
   int8_t *codes = reinterpret_cast<int8_t *>(smem + L.codes);
   float2 *sd = reinterpret_cast<float2 *>(smem + L.sd);
   float2 *terms = reinterpret_cast<float2 *>(smem + L.terms);
-  const uint8_t *base = W + (size_t)tile * nblk * kQ4kRecord;
+  const uint8_t *base = W + (size_t)gtile * nblk * kQ4kRecord;
   const bool arow = r < pg;  // this lane's A row (token r) exists
   // this lane's result tokens 4g + v, the sd row each reads (token 0 when past the group) and
   // where its terms go (a per-lane dummy slot when past the group)
@@ -159,7 +164,7 @@ __global__ __launch_bounds__(512) void q4k_i8route_kernel(
   for (int wb = 0; wb < nblk; wb += Wrec) {
     const int we = min(nblk, wb + Wrec), nw = we - wb;
     const int per = (nw + KW - 1) / KW;
-    const int b0 = min(we, wb + wave * per), b1 = min(we, b0 + per);
+    const int b0 = min(we, wb + kwave * per), b1 = min(we, b0 + per);
 
     // Loads are unconditional, re-reading the wave's last record (or the window's, for a wave
     // without records) where the ring runs past it: no branches around loads keeps the
@@ -210,7 +215,7 @@ __global__ __launch_bounds__(512) void q4k_i8route_kernel(
 
     // Rows of A past the group's tokens repeat token 0: their results are never read.
     const int8_t *arow_p = codes + (size_t)(arow ? r : 0) * L.cstride + 8 * g;
-    const bool chain = wave == 0;  // wave-uniform
+    const bool chain = kwave == 0;  // wave-uniform
     {
       // Every pass works kPF slots; slots past the wave's last record re-run that record (the
       // ring loads were clamped): their terms are rewritten with the same values and the chain
@@ -266,7 +271,7 @@ __global__ __launch_bounds__(512) void q4k_i8route_kernel(
       }
     }
     __syncthreads();
-    if (KW > 1 && wave == 0) {
+    if (KW > 1 && kwave == 0) {
       // the other waves' records of this window, in order: local records per .. nw - 1
       for (int k = 4 * min(per, nw); k < 4 * nw; ++k) {
 #pragma unroll
@@ -281,7 +286,7 @@ __global__ __launch_bounds__(512) void q4k_i8route_kernel(
     }
     __syncthreads();
   }
-  if (wave == 0) {
+  if (kwave == 0 && tile < ntiles) {
     const int row = tile * 16 + r;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
@@ -335,7 +340,7 @@ extern "C" int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, fl
   const int ntiles = q4k_tiles(out);
   const int groups = ceil_div(P, kTokGroup);
   const int pg = P < kTokGroup ? P : kTokGroup;
-  int KW = tuning().i8r_kw;
+  int KW = tuning().i8r_kw, TW = 1;
   if (KW <= 0) {
     KW = 1;
     const long long fill = (P == 1 ? 8LL : 16LL) * cu_count();
@@ -343,6 +348,19 @@ extern "C" int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, fl
       KW *= 2;
   }
   if (KW > 8) KW = 8;
+  // Wide matrices: one wave per tile and eight tiles per workgroup. The staged window (the
+  // tokens' codes) is quantized or copied once for the eight tiles and, with KW = 1, no terms are
+  // parked in LDS (18944 x 3584 at 1 / 4 / 8 / 16 tokens 18.8 / 41.0 / 43.3 / 45.4 us, against
+  // 21.3 / 76.1 / 91.1 / 144 with a tile of 2-4 waves per workgroup, whose parked terms held up to
+  // 155 KB of LDS, one workgroup per CU; 4 tiles per workgroup 20.7 / 44.7 / 44.7 / 48.1).
+  if (tuning().i8r_tw > 0) {
+    TW = tuning().i8r_tw;
+    KW = 1;
+  } else if (tuning().i8r_kw <= 0 && ntiles >= 4 * cu_count()) {
+    TW = 8;
+    KW = 1;
+  }
+  if (TW > 8) TW = 8;  // 512 threads per workgroup at most
   const size_t budget = (size_t)lds_limit();
   int wmax = nblk;
   while (wmax > 1 && i8r_lds(pg, wmax, KW).total > budget) --wmax;
@@ -352,11 +370,12 @@ extern "C" int fhip_q4k_matmul_int8_f32(const void *dPacked, const float *dX, fl
   if (lds > budget)
     return fail(FHIP_EINVAL, "fhip_q4k_matmul_int8_f32: %zu B of LDS exceeds the device limit",
                 lds);
-  dim3 grid(ntiles, groups);
+  dim3 grid(ceil_div(ntiles, TW), groups);
   // result tokens per lane: lane group g holds tokens 4g .. 4g + 3 of the group
   auto launch = [&](auto kern) {
-    kern<<<grid, 64 * KW, lds, stream()>>>(reinterpret_cast<const uint8_t *>(dPacked), dX, qx, sdg,
-                                           dY, out, in, nblk, P, Wrec, KW, fused ? 1 : 0);
+    kern<<<grid, 64 * KW * TW, lds, stream()>>>(reinterpret_cast<const uint8_t *>(dPacked), dX, qx,
+                                                sdg, dY, out, in, nblk, P, Wrec, KW, TW,
+                                                fused ? 1 : 0);
   };
   if (pg == 1)
     launch(q4k_i8route_kernel<1>);

@@ -238,6 +238,7 @@ int fhip_init(char *name, int namelen, int *arch, size_t *total_mem) {
   g_tuning.gemm32_sk = env_knob("FAK_HIP_GEMM32_SK");
   g_tuning.gemm32_nwb = env_knob("FAK_HIP_GEMM32_NWB");
   g_tuning.i8r_kw = env_knob("FAK_HIP_I8R_KW");
+  g_tuning.i8r_tw = env_knob("FAK_HIP_I8R_TW");
   g_tuning.q8_tw = env_knob("FAK_HIP_Q8_TW");
   g_tuning.q8_kw = env_knob("FAK_HIP_Q8_KW");
   if (name && namelen > 0) {

@@ -8,7 +8,7 @@ import pytest
 
 from fak_amd import fakhip, synth
 from tests import int8_cases as ic
-from tests.gpu_util import Dev, q4k_matmul_int8, rel_err
+from tests.gpu_util import Dev, knobs, q4k_matmul_int8, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -48,6 +48,31 @@ def test_matches_oracle(hip, oracle_mod, out, in_, P):
     Y = q4k_matmul_int8(raw, out, in_, X, P)
     ref = oracle_mod.q4k_gemm_int8(raw, out, in_, X, P)
     same_bits(Y, ref)
+
+
+@pytest.mark.parametrize("out,in_,P,tw", [(16400, 512, 5, 0), (16400, 512, 16, 0),
+                                          (100, 512, 16, 4), (100, 2304, 9, 8), (37, 1024, 3, 2),
+                                          (48, 18944, 17, 4), (64, 768, 1, 3)])
+def test_multi_tile_workgroups(hip, oracle_mod, monkeypatch, out, in_, P, tw):
+    """Several one-wave tiles per workgroup sharing its staged activations (the launch's choice
+    for wide matrices beyond four tokens, tw = 0: 16400 rows = 1025 tiles, the last workgroup
+    with one real tile; forced elsewhere with FAK_HIP_I8R_TW, ragged last workgroups, fused and
+    staged activations, windows of records): every output still bit-identical to the oracle."""
+    print(f"[case] int8 route tiles/wg={tw} out={out} in={in_} P={P}", flush=True)
+    raw = synth.q4k_weights(out, in_, out + 3 * in_ + P)
+    X = synth.activations(P, in_, P * 5 + 2)
+    if tw:
+        with knobs(monkeypatch, FAK_HIP_I8R_TW=tw):
+            Y = q4k_matmul_int8(raw, out, in_, X, P)
+    else:
+        Y = q4k_matmul_int8(raw, out, in_, X, P)
+    if out > 4096:
+        rb = (in_ // 256) * 144
+        sel = np.r_[0:80, out - 400:out]
+        sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
+        same_bits(Y[:, sel], oracle_mod.q4k_gemm_int8(sub, len(sel), in_, X, P))
+    else:
+        same_bits(Y, oracle_mod.q4k_gemm_int8(raw, out, in_, X, P))
 
 
 def test_reference_tolerance_vs_f32(hip, oracle_mod):
