@@ -272,17 +272,31 @@ __global__ __launch_bounds__(512) void q4k_i8route_kernel(
     }
     __syncthreads();
     if (KW > 1 && kwave == 0) {
-      // the other waves' records of this window, in order: local records per .. nw - 1
-      for (int k = 4 * min(per, nw); k < 4 * nw; ++k) {
+      // the other waves' records of this window, in order: local records per .. nw - 1. Eight
+      // pairs of sub-blocks are read before any is added, so the LDS latency is paid once per
+      // eight steps of the chain, not once per step (3584 x 18944 at one token: 31.6 -> 25.1 us).
+      auto step = [&](int v, const float4 p) {
+        acc[v] = __fadd_rn(acc[v], p.x);
+        acc[v] = __fsub_rn(acc[v], p.y);
+        acc[v] = __fadd_rn(acc[v], p.z);
+        acc[v] = __fsub_rn(acc[v], p.w);
+      };
+      int k = 4 * min(per, nw);
+      const int kend = 4 * nw;
+      for (; k + 8 <= kend; k += 8) {
+        float4 p[8][NV];
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-          const float4 p = reinterpret_cast<const float4 *>(tdst[v])[k];
-          acc[v] = __fadd_rn(acc[v], p.x);
-          acc[v] = __fsub_rn(acc[v], p.y);
-          acc[v] = __fadd_rn(acc[v], p.z);
-          acc[v] = __fsub_rn(acc[v], p.w);
-        }
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int v = 0; v < NV; ++v) p[j][v] = reinterpret_cast<const float4 *>(tdst[v])[k + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int v = 0; v < NV; ++v) step(v, p[j][v]);
       }
+      for (; k < kend; ++k)
+#pragma unroll
+        for (int v = 0; v < NV; ++v) step(v, reinterpret_cast<const float4 *>(tdst[v])[k]);
     }
     __syncthreads();
   }
