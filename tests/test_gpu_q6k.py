@@ -76,6 +76,24 @@ def test_gemv_matches_oracle(hip, oracle_mod, out, in_, P):
     assert err <= 1e-3
 
 
+@pytest.mark.parametrize("pattern", ["big", "tiny", "wee", "mixed", "outlier"])
+@pytest.mark.parametrize("out,in_,P", [(1024, 2048, 1), (3584, 18944, 1), (1024, 2048, 4),
+                                       (1024, 2048, 16), (512, 2048, 40)])
+def test_activation_scales(hip, oracle_mod, out, in_, P, pattern):
+    """Q6_K on activations far outside f16 (x 1e5, a lone 7e4), far below it (x 1e-20, x 1e-35)
+    and mixed within a row: every token row within its route's bound of the oracle (1e-3 up to
+    16 tokens, 1e-2 on the GEMM), judged per row."""
+    from tests.gpu_util import rel_err_rows, scaled_activations
+    print(f"[case] q6k scales out={out} in={in_} P={P} {pattern}", flush=True)
+    rng = np.random.default_rng(out + in_ + P)
+    raw = qc.pin_d(rng.integers(0, 256, size=out * (in_ // 256) * 210, dtype=np.uint8), 0x1400)
+    X = scaled_activations(P, in_, 7 * P + 3, pattern)
+    Y = dev_matmul(raw, out, in_, X, P)
+    e = rel_err_rows(Y, oracle_mod.q6k_gemm(raw, out, in_, X, P))
+    print(f"    per-row max|d|/RMS = {e:.3e}", flush=True)
+    assert e <= (1e-3 if P <= 16 else 1e-2), e
+
+
 @pytest.mark.parametrize("out,in_", [(1, 256), (16, 512), (37, 768), (300, 1024)])
 def test_repack_round_trip(hip, out, in_):
     """The tiled layout is a byte permutation: repack then unpack returns the raw rows, and
