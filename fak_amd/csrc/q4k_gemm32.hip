@@ -522,7 +522,7 @@ constexpr int gemm32s_wait(int fmt, int ls, int kdma) {
   return fmt == 0 ? 2 * kdma
                   : 2 * kdma + (ls <= 2 ? 6 : 0) + (ls >= 4 && ls <= 6 ? 8 : 0);
 }
-template <int FMT, int WPE>
+template <int FMT, int WPE, int NTW>
 __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void quant_gemm32s_kernel(
     const uint8_t *__restrict__ W, const uint4 *__restrict__ xa,
     const float *__restrict__ tscale, float *__restrict__ Y, int N,
@@ -530,7 +530,9 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
   constexpr int NW = kGemmWaves;
   constexpr int kUnits = kQ4kRecord / 16;                       // 144 units per Q4_K record
   constexpr int kSU = 4 * 2 * 64;                               // 512 units (8 KB) per stage
-  constexpr int NT = 4 / NW;                                    // 32-row MFMA tiles per wave
+  constexpr int NT = NTW;                                       // 32-row MFMA tiles per wave
+  constexpr int kBTn = 2 * NT * NW;                             // 16-row tiles per workgroup
+  constexpr int kRT = 16 * kBTn;                                // rows per workgroup tile
   constexpr int kDMA = 8 / NW;                                  // stage loads per wave
   // Four named arrays, not one indexed array: the compiler tracks LDS DMA per object, so a read
   // of one stage does not wait for the DMA into another.
@@ -554,7 +556,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
   const int nq = nblk * 16;
   const Magic K = magic_consts();
   const u32x4 *xg = reinterpret_cast<const u32x4 *>(xa) + (size_t)(4 * mg) * nq * 64;
-  const int tile0 = kBT * ng;
+  const int tile0 = kBTn * ng;
   // Stage s = 8 b + 2 c + h: slices 16 (4 b + c) + h + 2 hi of token tile i at [(2 i + hi) * 64],
   // one 1 KB wave load each; wave w loads units kDMA w .. kDMA w + kDMA - 1 (unit 2 i + hi).
   auto load_stage = [&](int s, u32x4 *dst) {
@@ -575,7 +577,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
   // int8 scales and f16 d, and per half hh of the super-block (chunks 2 hh, 2 hh + 1) the lane's
   // 8 ql bytes of each of the four groups and 8 qh bytes of each K16 half. Rows past N read the
   // last tile.
-  auto tl = [&](int t) { return (8 / NW) * wave + 2 * t + (rho >> 4); };
+  auto tl = [&](int t) { return 2 * NT * wave + 2 * t + (rho >> 4); };
   const int r16 = rho & 15;
   const u32x4 *Wv = reinterpret_cast<const u32x4 *>(W);
   auto rec = [&](int t, int b) {
@@ -733,10 +735,11 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
             for (int t = 0; t < NT; ++t)
               acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, hi ? bh[t] : bl[t], acc[i][t], 0, 0, 0);
           }
-          // Q6_K: the second K16 half's operand reads wait for the first half's MFMAs, and each
-          // stage's code words enter through fresh pinned copies: so scheduled the kernel needs
-          // 145 VGPRs and runs three workgroups per CU (219, and two, before).
-          if (FMT == 1 && hi == 0) __builtin_amdgcn_sched_barrier(0);
+          // Q6_K, and 64 rows per wave: the second K16 half's operand reads wait for the first
+          // half's MFMAs (and Q6_K's code words enter each stage through fresh pinned copies):
+          // so scheduled Q6_K needs 145 VGPRs and runs three workgroups per CU (219, and two,
+          // before), and 64 rows per wave fit 256 VGPRs without a spill.
+          if ((FMT == 1 || NT == 2) && hi == 0) __builtin_amdgcn_sched_barrier(0);
         }
         // Stage s + 1 has landed (for every wave, after the barrier) once at most stages s + 2
         // and s + 3 (kDMA loads each) and the record loads that gemm32s_wait allows are
@@ -770,7 +773,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int o = 16 * (kBT * ng + (8 / NW) * wave + 2 * t) + rho;
+      const int o = 16 * (kBTn * ng + 2 * NT * wave + 2 * t) + rho;
       if (o >= N) continue;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
@@ -780,8 +783,8 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
         if (sp == 0)
           Y[(size_t)tok * N + o] = val;
         else
-          part[((size_t)(sp - 1) * R + (task - F)) * kTileElems + (tok - kBM * mg) * 128 +
-               (o - 128 * ng)] = val;
+          part[((size_t)(sp - 1) * R + (task - F)) * (kBM * kRT) + (tok - kBM * mg) * kRT +
+               (o - kRT * ng)] = val;
       }
     }
   }
@@ -790,17 +793,19 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
 
 
 // Y += the partial sums of K ranges 1 .. S-1 of the R split tiles (tasks F .. F+R-1), added in
-// range order after range 0, which the GEMM wrote to Y (deterministic). part holds 128 x 128
-// f32 per (range, tile), token-major. Each thread adds four outputs of one token row.
+// range order after range 0, which the GEMM wrote to Y (deterministic). part holds 128 x RT
+// f32 per (range, tile), token-major (RT: the workgroup tile's rows, 128 or 256). Each thread
+// adds four outputs of one token row.
+template <int RT>
 __global__ __launch_bounds__(256) void gemm32_reduce_kernel(const float *__restrict__ part,
                                                             float *__restrict__ Y, int N, int M,
                                                             int MTG, int F, int S, int R) {
-  constexpr int kQuads = kTileElems / 4;
+  constexpr int kQuads = kBM * RT / 4;
   const long long id = (long long)blockIdx.x * 256 + threadIdx.x;
   if (id >= (long long)R * kQuads) return;
   const int r = (int)(id / kQuads), e4 = (int)(id - (long long)r * kQuads);
   const int task = F + r, mg = task % MTG, ng = task / MTG;
-  const int tok = kBM * mg + (e4 >> 5), o0 = 128 * ng + 4 * (e4 & 31);
+  const int tok = kBM * mg + e4 / (RT / 4), o0 = RT * ng + 4 * (e4 % (RT / 4));
   if (tok >= M || o0 >= N) return;
   // Range s (1 .. S-1) of this tile's quad: part + ((s - 1) R + r) kQuads + e4.
   const float4 *pp = reinterpret_cast<const float4 *>(part) + (size_t)r * kQuads + e4;
@@ -833,6 +838,7 @@ namespace {
 // token scales, then the K-range partial results).
 struct GemmPlan {
   int MTG, tasks, form, F, S, R;  // tile tasks; F whole, then R split into S K ranges each
+  int nt;                         // 32-row MFMA tiles per wave: 1 (128-row tiles) or 2 (256)
   size_t xab, tsb, pb;
 };
 
@@ -840,11 +846,25 @@ GemmPlan plan_gemm32(int fmt, int N, int K, int M) {
   GemmPlan p{};
   const int nblk = K / 256;
   p.MTG = ceil_div(M, kBM);
-  p.tasks = p.MTG * ceil_div(q4k_tiles(N), kBT);
   // FAK_HIP_GEMM32_FORM=1: the four-wave 2x2 kernel (a comparison; it agrees bit for bit with
   // the default without a K split). Default: the staged kernel, measured faster from 64 to 2048
   // tokens.
   p.form = tuning().gemm32_form;
+  const int cus = cu_count() > 0 ? cu_count() : 256;
+  // Q4_K on the staged kernel from eight token tiles (M > 896) takes 256-row workgroups (four
+  // waves of 64 rows, two workgroups per CU): each staged activation byte then feeds twice the
+  // MFMAs. Same box, gate/up shape, M = 1024 / 2048 / 4096: 175-178 / 320 / 582 us against
+  // 181-183 / 333-337 / 618-621 with 128-row tiles; the down shape at M=2048 361 against 371.
+  // With fewer token tiles the uneven spread of fewer, larger tiles costs more (M=512: gate/up
+  // 100-103 against 96, down 117 against 112). FAK_HIP_GEMM32_NT=1 / 2 forces the choice.
+  p.nt = 1;
+  if (fmt == 0 && p.form != 1) {
+    if (tuning().gemm32_nt == 1 || tuning().gemm32_nt == 2)
+      p.nt = tuning().gemm32_nt;
+    else if (tuning().gemm32_sk <= 0 && p.MTG >= 8)
+      p.nt = 2;
+  }
+  p.tasks = p.MTG * ceil_div(q4k_tiles(N), kBT * p.nt);
   p.F = p.tasks;
   p.S = 1;
   p.R = 0;
@@ -861,7 +881,6 @@ GemmPlan plan_gemm32(int fmt, int N, int K, int M) {
     //    range (M=512 on the gate/up shape: 512 whole tiles and 80 tiles in 3 ranges, where 80
     //    CUs ran a third whole tile; ranges of at least 2 super-blocks);
     //  * FAK_HIP_GEMM32_SK=n splits every tile in n (1: no split).
-    const int cus = cu_count() > 0 ? cu_count() : 256;
     const int sk = tuning().gemm32_sk;
     int S = 1, R = 0;
     if (sk > 0) {
@@ -882,7 +901,7 @@ GemmPlan plan_gemm32(int fmt, int N, int K, int M) {
   }
   p.xab = ((size_t)p.MTG * kBM * K * 2 + 255) & ~(size_t)255;
   p.tsb = ((size_t)p.MTG * kBM * 4 + 255) & ~(size_t)255;
-  p.pb = p.R ? (size_t)(p.S - 1) * p.R * kTileElems * 4 : 0;
+  p.pb = p.R ? (size_t)(p.S - 1) * p.R * kTileElems * p.nt * 4 : 0;
   return p;
 }
 
@@ -902,16 +921,20 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
   const uint8_t *W = (const uint8_t *)Wv;
   auto reduce = [&]() -> int {
     if (p.R) {
-      const long long quads = (long long)p.R * (kTileElems / 4);
-      gemm32_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, stream()>>>(
-          part, Y, N, M, MTG, p.F, p.S, p.R);
+      const long long quads = (long long)p.R * (kTileElems * p.nt / 4);
+      if (p.nt == 2)
+        gemm32_reduce_kernel<256><<<(unsigned)((quads + 255) / 256), 256, 0, stream()>>>(
+            part, Y, N, M, MTG, p.F, p.S, p.R);
+      else
+        gemm32_reduce_kernel<128><<<(unsigned)((quads + 255) / 256), 256, 0, stream()>>>(
+            part, Y, N, M, MTG, p.F, p.S, p.R);
       FHIP_CHECK_LAUNCH("gemm32_reduce_kernel");
     }
     return FHIP_OK;
   };
   const int grid2 = p.F + p.R * p.S;
   if (fmt == 1 && p.form != 1) {
-    quant_gemm32s_kernel<1, 3><<<grid2, 64 * kGemmWaves, 0, stream()>>>(
+    quant_gemm32s_kernel<1, 3, 1><<<grid2, 64 * kGemmWaves, 0, stream()>>>(
         W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
     FHIP_CHECK_LAUNCH("quant_gemm32s_kernel<1>");
     return reduce();
@@ -923,8 +946,12 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
     return reduce();
   }
   if (p.form != 1) {
-    quant_gemm32s_kernel<0, 3><<<grid2, 64 * kGemmWaves, 0, stream()>>>(
-        W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
+    if (p.nt == 2)
+      quant_gemm32s_kernel<0, 2, 2><<<grid2, 64 * kGemmWaves, 0, stream()>>>(
+          W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
+    else
+      quant_gemm32s_kernel<0, 3, 1><<<grid2, 64 * kGemmWaves, 0, stream()>>>(
+          W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
     FHIP_CHECK_LAUNCH("quant_gemm32s_kernel<0>");
     return reduce();
   }

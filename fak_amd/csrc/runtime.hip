@@ -235,6 +235,7 @@ int fhip_init(char *name, int namelen, int *arch, size_t *total_mem) {
   const int from16 = env_knob("FAK_HIP_GEMV16_FROM");
   g_tuning.gemv16_from = from16 >= 1 && from16 <= 5 ? from16 : 0;
   g_tuning.gemm32_form = env_knob("FAK_HIP_GEMM32_FORM");
+  g_tuning.gemm32_nt = env_knob("FAK_HIP_GEMM32_NT");
   g_tuning.gemm32_sk = env_knob("FAK_HIP_GEMM32_SK");
   g_tuning.gemm32_nwb = env_knob("FAK_HIP_GEMM32_NWB");
   g_tuning.i8r_kw = env_knob("FAK_HIP_I8R_KW");

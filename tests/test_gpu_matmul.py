@@ -273,6 +273,25 @@ def test_q4k_gemm_forms_bit_identical(hip, oracle_mod, monkeypatch, out, in_, P)
     assert rel_err(got, ref) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("out,in_,P", [(18944, 3584, 2048), (18900, 1024, 2100)])
+def test_q4k_gemm_wide_tiles(hip, oracle_mod, monkeypatch, out, in_, P):
+    """From eight token tiles (M > 896) the staged kernel takes 256-row workgroups (four waves of
+    64 rows). Every output keeps the 128-row kernel's MFMA sequence, so the result is
+    bit-identical to the unsplit four-wave 2x2 form, on whole and ragged row and token tiles, and
+    meets the GEMM bound on rows spread over every row tile."""
+    print(f"[case] gemm wide tiles out={out} in={in_} P={P}", flush=True)
+    raw = synth.q4k_weights(out, in_, seed=out + 5 * P)
+    X = synth.activations(P, in_, seed=P + 19)
+    Y = q4k_matmul(raw, out, in_, X, P)
+    with knobs(monkeypatch, FAK_HIP_GEMM32_FORM=1, FAK_HIP_GEMM32_SK=1):
+        Y1 = q4k_matmul(raw, out, in_, X, P)
+    assert np.array_equal(Y.view(np.uint32), Y1.view(np.uint32))
+    rb = (in_ // 256) * 144
+    sel = spread_rows(out, per_block=1)
+    sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
+    assert rel_err(Y[:, sel], oracle_mod.q4k_gemm(sub, len(sel), in_, X, P, workers=16)) <= GEMM_TOL
+
+
 @pytest.mark.parametrize("out,in_,P", [(3584, 18944, 512), (1000, 2048, 520), (18944, 3584, 128),
                                        (300, 4096, 40)])
 def test_q4k_gemm_k_split(hip, oracle_mod, out, in_, P):
