@@ -63,7 +63,7 @@ struct Tuning {
   int gemv_globalx;       // FAK_HIP_GEMV_GLOBALX: activation operands in global memory
   int gemv16_from;        // FAK_HIP_GEMV16_FROM: first width on the 5..16-token kernel (1..5)
   int gemm32_form;        // FAK_HIP_GEMM32_FORM: 1 = four-wave 2x2 (else the staged kernel)
-  int gemm32_nt;          // FAK_HIP_GEMM32_NT: 32-row tiles per wave of the staged Q4_K kernel
+  int gemm32_nt;          // FAK_HIP_GEMM32_NT: 32-row tiles per wave of the staged kernel
   int gemm32_sk;          // FAK_HIP_GEMM32_SK: K ranges of the prefill GEMM
   int gemm32_nwb;         // FAK_HIP_GEMM32_NWB: weight buffers of the 2x2 form (1 or 2)
   int i8r_kw;             // FAK_HIP_I8R_KW: waves per tile of the int8 route

@@ -512,15 +512,16 @@ constexpr int wait_vm(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }  /
 // (256 VGPRs, two per SIMD) measured slower at every size (M=512 112.7 against 106.5 us, M=2048
 // 413 against 376, with the records still in LDS) and no longer fit their registers.
 constexpr int kGemmWaves = 4;
-// Loads a wave may leave pending at the end of stage ls (0..7) of a super-block: the DMA of the
-// two later stages (kdma each), and for Q6_K the record group issued at stage 0 (6 loads)
-// through stage 2 and the one issued at stage 4 (8 loads) through stage 6. Q4_K's records (2
-// and 3 loads) complete within the stage after their issue: with plain loads pending beside
-// the LDS DMA the compiler no longer trusts the counter's order and drains it (vmcnt(0)) before
-// the next read of a DMA buffer, twice per super-block, which measured the same.
-constexpr int gemm32s_wait(int fmt, int ls, int kdma) {
-  return fmt == 0 ? 2 * kdma
-                  : 2 * kdma + (ls <= 2 ? 6 : 0) + (ls >= 4 && ls <= 6 ? 8 : 0);
+// Loads a wave may leave pending at the end of stage ls (0..7) of a super-block, with nt 32-row
+// tiles per wave: the DMA of the two later stages (kdma each), and for Q6_K the record group
+// issued at stage 0 (6 nt loads) through stage 2 and the one issued at stage 4 (8 nt loads)
+// through stage 6. Q4_K's records (2 nt and 3 nt loads) complete within the stage after their
+// issue: with plain loads pending beside the LDS DMA the compiler no longer trusts the counter's
+// order and drains it (vmcnt(0)) before the next read of a DMA buffer, twice per super-block,
+// which measured the same.
+constexpr int gemm32s_wait(int fmt, int nt, int ls, int kdma) {
+  return fmt == 0 ? 2 * kdma + (ls <= 1 ? 2 * (nt - 1) : 0) + (ls == 4 || ls == 5 ? 3 * (nt - 1) : 0)
+                  : 2 * kdma + (ls <= 2 ? 6 * nt : 0) + (ls >= 4 && ls <= 6 ? 8 * nt : 0);
 }
 template <int FMT, int WPE, int NTW>
 __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void quant_gemm32s_kernel(
@@ -745,14 +746,14 @@ __global__ __launch_bounds__(64 * kGemmWaves) __attribute__((amdgpu_waves_per_eu
         // and s + 3 (kDMA loads each) and the record loads that gemm32s_wait allows are
         // pending.
         switch (ls) {
-          case 0: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 0, kDMA))); break;
-          case 1: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 1, kDMA))); break;
-          case 2: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 2, kDMA))); break;
-          case 3: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 3, kDMA))); break;
-          case 4: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 4, kDMA))); break;
-          case 5: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 5, kDMA))); break;
-          case 6: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 6, kDMA))); break;
-          default: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, 7, kDMA))); break;
+          case 0: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, NT, 0, kDMA))); break;
+          case 1: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, NT, 1, kDMA))); break;
+          case 2: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, NT, 2, kDMA))); break;
+          case 3: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, NT, 3, kDMA))); break;
+          case 4: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, NT, 4, kDMA))); break;
+          case 5: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, NT, 5, kDMA))); break;
+          case 6: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, NT, 6, kDMA))); break;
+          default: FHIP_LDS_BARRIER(wait_vm(gemm32s_wait(FMT, NT, 7, kDMA))); break;
         }
       }
     }
@@ -851,14 +852,16 @@ GemmPlan plan_gemm32(int fmt, int N, int K, int M) {
   // tokens.
   p.form = tuning().gemm32_form;
   const int cus = cu_count() > 0 ? cu_count() : 256;
-  // Q4_K on the staged kernel from eight token tiles (M > 896) takes 256-row workgroups (four
-  // waves of 64 rows, two workgroups per CU): each staged activation byte then feeds twice the
-  // MFMAs. Same box, gate/up shape, M = 1024 / 2048 / 4096: 175-178 / 320 / 582 us against
-  // 181-183 / 333-337 / 618-621 with 128-row tiles; the down shape at M=2048 361 against 371.
-  // With fewer token tiles the uneven spread of fewer, larger tiles costs more (M=512: gate/up
-  // 100-103 against 96, down 117 against 112). FAK_HIP_GEMM32_NT=1 / 2 forces the choice.
+  // The staged kernel from eight token tiles (M > 896) takes 256-row workgroups (four waves of
+  // 64 rows, two workgroups per CU): each staged activation byte then feeds twice the MFMAs.
+  // Same box, Q4_K gate/up shape, M = 1024 / 2048 / 4096: 175-178 / 320 / 582 us against
+  // 181-183 / 333-337 / 618-621 with 128-row tiles; the down shape at M=2048 361 against 371;
+  // Q6_K gate/up at M = 1024 / 2048 207-210 / 374 against 215 / 381, down 231 / 413 against
+  // 242 / 440. With fewer token tiles the uneven spread of fewer, larger tiles costs more
+  // (M=512: Q4_K gate/up 100-103 against 96, down 117 against 112). FAK_HIP_GEMM32_NT=1 / 2
+  // forces the choice.
   p.nt = 1;
-  if (fmt == 0 && p.form != 1) {
+  if (p.form != 1) {
     if (tuning().gemm32_nt == 1 || tuning().gemm32_nt == 2)
       p.nt = tuning().gemm32_nt;
     else if (tuning().gemm32_sk <= 0 && p.MTG >= 8)
@@ -934,8 +937,12 @@ int launch_gemm32(int fmt, const void *Wv, const float *X, float *Y, int N, int 
   };
   const int grid2 = p.F + p.R * p.S;
   if (fmt == 1 && p.form != 1) {
-    quant_gemm32s_kernel<1, 3, 1><<<grid2, 64 * kGemmWaves, 0, stream()>>>(
-        W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
+    if (p.nt == 2)
+      quant_gemm32s_kernel<1, 2, 2><<<grid2, 64 * kGemmWaves, 0, stream()>>>(
+          W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
+    else
+      quant_gemm32s_kernel<1, 3, 1><<<grid2, 64 * kGemmWaves, 0, stream()>>>(
+          W, xa, ts, Y, N, M, nblk, ntiles, MTG, p.F, p.S, p.R, part);
     FHIP_CHECK_LAUNCH("quant_gemm32s_kernel<1>");
     return reduce();
   }

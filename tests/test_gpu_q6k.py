@@ -174,3 +174,26 @@ def test_gemm_forms_bit_identical(hip, oracle_mod, monkeypatch, out, in_, P):
     err = rel_err(Y2[:, sel], oracle_mod.q6k_gemm(sub, len(sel), in_, X, P))
     print(f"    max|d|/RMS = {err:.2e}", flush=True)
     assert err <= 1e-2
+
+
+@pytest.mark.parametrize("out,in_,P", [(18944, 3584, 2048), (18900, 1024, 1100)])
+def test_gemm_wide_tiles(hip, oracle_mod, monkeypatch, out, in_, P):
+    """From eight token tiles (M > 896) the staged Q6_K kernel takes 256-row workgroups (four
+    waves of 64 rows). Each output keeps the 128-row kernel's MFMA sequence: on grids that the
+    plan leaves without a K split (1184 and 666 workgroups on 256 CUs), bit-identical to the
+    unsplit four-wave 2x2 form on whole and ragged row and token tiles, and within the GEMM bound
+    of the oracle on rows spread over every row tile."""
+    print(f"[case] q6k gemm wide tiles out={out} in={in_} P={P}", flush=True)
+    rng = np.random.default_rng(out + 5 * P)
+    raw = qc.pin_d(rng.integers(0, 256, size=out * (in_ // 256) * 210, dtype=np.uint8), 0x1400)
+    X = rng.standard_normal((P, in_)).astype(np.float32)
+    Y = dev_matmul(raw, out, in_, X, P)
+    with knobs(monkeypatch, FAK_HIP_GEMM32_FORM=1, FAK_HIP_GEMM32_SK=1):
+        Y1 = dev_matmul(raw, out, in_, X, P)
+    assert np.array_equal(Y.view(np.uint32), Y1.view(np.uint32))
+    rb = (in_ // 256) * 210
+    sel = spread_rows(out, per_block=1)
+    sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
+    err = rel_err(Y[:, sel], oracle_mod.q6k_gemm(sub, len(sel), in_, X, P))
+    print(f"    max|d|/RMS = {err:.2e}", flush=True)
+    assert err <= 1e-2
