@@ -293,11 +293,13 @@ def test_q4k_gemm_wide_tiles(hip, oracle_mod, monkeypatch, out, in_, P):
 
 
 @pytest.mark.parametrize("out,in_,P", [(3584, 18944, 512), (1000, 2048, 520), (18944, 3584, 128),
-                                       (300, 4096, 40)])
+                                       (300, 4096, 40), (3584, 18944, 1024), (3000, 18944, 1000)])
 def test_q4k_gemm_k_split(hip, oracle_mod, out, in_, P):
     """Grids too small for the GPU split K and add the ranges' partial sums in range order: the
     result meets the GEMM bound against the oracle (sampled rows for the 7B shapes) and is the
-    same bits call after call."""
+    same bits call after call. From eight token tiles the split tiles are the 256-row ones (the
+    7B down projection at 1024 tokens: 112 tiles in 4 ranges; 3000 rows and 1000 tokens: ragged
+    row and token tiles in 5 ranges)."""
     print(f"[case] gemm k split out={out} in={in_} P={P}", flush=True)
     raw = synth.q4k_weights(out, in_, seed=out + 7 * P)
     X = synth.activations(P, in_, seed=P + 11)

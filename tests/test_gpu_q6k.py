@@ -129,11 +129,13 @@ def test_argument_errors(hip):
                                             (3584, 18944, 24, 48), (152, 4096, 32, None),
                                             (37, 256, 19, None), (1000, 2048, 28, None),
                                             (1000, 2048, 200, 64), (18944, 3584, 512, 64),
-                                            (3584, 18944, 128, 48)])
+                                            (3584, 18944, 128, 48), (3584, 18944, 1024, 48),
+                                            (3000, 18944, 1000, 48)])
 def test_gemm_prefill_matches_oracle(hip, oracle_mod, out, in_, P, rows):
     """More than 16 tokens (17..32 on the small-M kernel's f16 form, more on the f16 MFMA prefill
-    GEMM) on the Q6_K records: max|dY|/RMS <= 1e-2 (the GEMM bound), checked on every output or
-    on a sample of rows at full shape."""
+    GEMM, its 256-row workgroups with K ranges from eight token tiles on the long rows) on the
+    Q6_K records: max|dY|/RMS <= 1e-2 (the GEMM bound), checked on every output or on a sample
+    of rows at full shape."""
     print(f"[case] q6k gemm out={out} in={in_} P={P}", flush=True)
     rng = np.random.default_rng(out + 7 * in_ + P)
     raw = qc.pin_d(rng.integers(0, 256, size=out * (in_ // 256) * 210, dtype=np.uint8), 0x1400)
