@@ -324,12 +324,14 @@ def test_q4k_gemm_tail_split(hip, oracle_mod, monkeypatch, out, in_, P):
     last, partial round's tiles into K ranges (range 0 in Y, the rest added in range order). On
     ragged row and token tiles: the first row block (whole tiles) is bit-identical to the
     unsplit kernel, the last rows (split tiles) meet the GEMM bound against the oracle, and the
-    result is the same bits call after call."""
+    result is the same bits call after call. (128-row workgroups throughout: from eight token
+    tiles the default takes 256-row ones, whose 1184 tiles at 2048 tokens need no split.)"""
     print(f"[case] gemm tail split out={out} in={in_} P={P}", flush=True)
     raw = synth.q4k_weights(out, in_, seed=out + 13 * P)
     X = synth.activations(P, in_, seed=P + 17)
-    Y = q4k_matmul(raw, out, in_, X, P)
-    assert np.array_equal(Y.view(np.uint32), q4k_matmul(raw, out, in_, X, P).view(np.uint32))
+    with knobs(monkeypatch, FAK_HIP_GEMM32_NT=1):
+        Y = q4k_matmul(raw, out, in_, X, P)
+        assert np.array_equal(Y.view(np.uint32), q4k_matmul(raw, out, in_, X, P).view(np.uint32))
     with knobs(monkeypatch, FAK_HIP_GEMM32_SK=1):
         Y1 = q4k_matmul(raw, out, in_, X, P)
     assert np.array_equal(Y[:, :128].view(np.uint32), Y1[:, :128].view(np.uint32))
