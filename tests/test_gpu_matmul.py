@@ -343,6 +343,28 @@ def test_q4k_gemm_tail_split(hip, oracle_mod, monkeypatch, out, in_, P):
     assert rel_err(Y[:, out - 112:], Y1[:, out - 112:]) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("out,in_,P", [(18944, 3584, 1024), (18900, 3584, 1000)])
+def test_q4k_gemm_tail_split_wide(hip, oracle_mod, monkeypatch, out, in_, P):
+    """The tail split on 256-row workgroups (eight token tiles, 592 tiles: 512 whole, the last 80
+    in 3 K ranges), on whole and ragged row and token tiles: the first row block is
+    bit-identical to the unsplit 128-row kernel, sampled rows of every row block and the last
+    rows meet the GEMM bound against the oracle, and the result is the same bits call after
+    call."""
+    print(f"[case] gemm tail split wide out={out} in={in_} P={P}", flush=True)
+    raw = synth.q4k_weights(out, in_, seed=out + 3 * P)
+    X = synth.activations(P, in_, seed=P + 23)
+    Y = q4k_matmul(raw, out, in_, X, P)
+    assert np.array_equal(Y.view(np.uint32), q4k_matmul(raw, out, in_, X, P).view(np.uint32))
+    with knobs(monkeypatch, FAK_HIP_GEMM32_SK=1):
+        Y1 = q4k_matmul(raw, out, in_, X, P)
+    assert np.array_equal(Y[:, :256].view(np.uint32), Y1[:, :256].view(np.uint32))
+    rb = (in_ // 256) * 144
+    sel = np.unique(np.concatenate([spread_rows(out, per_block=1), np.arange(out - 64, out)]))
+    sub = np.concatenate([raw[o * rb:(o + 1) * rb] for o in sel])
+    ref = oracle_mod.q4k_gemm(sub, len(sel), in_, X, P, workers=16)
+    assert rel_err(Y[:, sel], ref) <= GEMM_TOL
+
+
 def test_q4k_gemm_equals_gemv_per_token_within_tolerance(hip, oracle_mod):
     """The reference pins GEMM(o,t) == GEMV(X_t)(o) bitwise on the CPU; on the device the two
     kernels use different precisions, so each is held to its own bound against the same oracle

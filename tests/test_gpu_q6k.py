@@ -130,7 +130,7 @@ def test_argument_errors(hip):
                                             (37, 256, 19, None), (1000, 2048, 28, None),
                                             (1000, 2048, 200, 64), (18944, 3584, 512, 64),
                                             (3584, 18944, 128, 48), (3584, 18944, 1024, 48),
-                                            (3000, 18944, 1000, 48)])
+                                            (3000, 18944, 1000, 48), (18944, 3584, 1024, 64)])
 def test_gemm_prefill_matches_oracle(hip, oracle_mod, out, in_, P, rows):
     """More than 16 tokens (17..32 on the small-M kernel's f16 form, more on the f16 MFMA prefill
     GEMM, its 256-row workgroups with K ranges from eight token tiles on the long rows) on the
