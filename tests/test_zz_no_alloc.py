@@ -20,14 +20,15 @@ def run(fn, w, X, out, in_, P):
 # (out, in, P): a K-split prefill GEMM (operands + token scales + partials: ~56 MB of scratch),
 # then smaller calls: a 16-token GEMV with K-range partials, a 3-token GEMV with global
 # activation operands, one decode token, a 24-token call (the 17..32-token route, K-range
-# partials sized for its tokens) and a 4-token call at in >= 24576 (which takes the 5..16-token
-# kernel's route from three tokens).
+# partials sized for its tokens), a 4-token call at in >= 24576 (which takes the 5..16-token
+# kernel's route from three tokens) and a 1024-token GEMM on 256-row workgroups in 4 K ranges
+# (~52 MB of scratch).
 CALLS = [(3584, 18944, 512), (2048, 6144, 16), (3584, 18944, 3), (1024, 3584, 1),
-         (18944, 3584, 24), (5120, 25600, 4)]
+         (18944, 3584, 24), (5120, 25600, 4), (3584, 4096, 1024)]
 
 
 @pytest.mark.parametrize("first,second", [(0, 1), (1, 2), (2, 3), (0, 3), (0, 4), (4, 5),
-                                          (5, 3)])
+                                          (5, 3), (6, 0), (6, 1)])
 def test_noalloc_matches_allocating_entry(hip, oracle_mod, first, second):
     lib = fakhip.load()
     for idx in (first, second):
