@@ -302,7 +302,7 @@ def bench_gemv_pair(steps, warmup, ev, seed=7):
     disp = [time_dispatch(c, steps, warmup, ev) for c in calls]
     alone = [time_dispatch(c, steps, warmup, ev, isolated=True) for c in calls]
     # correctness: every output of both shapes against the oracle on the same inputs
-    import oracle  # the checker
+    import oracle  # the oracle: the reference results
     checks = []
     for w, (x, xb), yb in zip(ws, xs, ys):
         fakhip.call("fhip_q4k_matmul_f32", w.ptrs[0], xb.ptr, yb.ptr, w.n, w.k, 1)
@@ -344,7 +344,7 @@ def bench_q8_0(steps, warmup, ev, graph_copies=300):
     gcalls = [("fhip_q8_0_matmul_f32", lambda i, j=j: (w.ptrs[j], xb.ptr, yb.ptr, n, k, 1))
               for j in range(graph_copies)]
     graph_ms = decode_graph_ms(gcalls, max(5, steps // 20), 2, ev)
-    import oracle  # the checker
+    import oracle  # the oracle: the reference results
     fakhip.call("fhip_q8_0_matmul_f32", w.ptrs[0], xb.ptr, yb.ptr, n, k, 1)
     chk = check(yb.host(), oracle.q8_0_matrows(w.raw, n, k, x[0]))
     w.free(), xb.free(), yb.free()
@@ -368,7 +368,7 @@ def bench_gemm(M, steps, warmup, ev):
     ms, per = time_calls(calls, steps, warmup, ev)
     flops = 2.0 * M * n * k
     t = ms * 1e-3  # back to back: one call per step
-    import oracle  # the checker
+    import oracle  # the oracle: the reference results
     fakhip.call("fhip_q4k_matmul_f32", w.ptrs[0], xb.ptr, yb.ptr, n, k, M)
     sub, sel = spread_sample(w.raw, n, k)
     chk = check(yb.host().reshape(M, n)[:, sel], oracle.q4k_gemm(sub, len(sel), k, X, M,
@@ -384,7 +384,7 @@ def bench_gemm(M, steps, warmup, ev):
 def bench_small_m(steps, warmup, ev):
     """C5: the 27B-class FFN pair (gate/up 5120 -> 25600, down 25600 -> 5120) at the verify widths
     M = 1, 4, 8, 16; every output of both shapes checked."""
-    import oracle  # the checker
+    import oracle  # the oracle: the reference results
     out = []
     cpu_in = []
     shapes = [(25600, 5120), (5120, 25600)]
@@ -628,7 +628,7 @@ def bench_decode_stack(steps, warmup, ev, layers=28):
     wbytes = layers * sum(q4k_bytes(n, k) for n, k in layer_shapes) + q4k_bytes(V, H)
     abytes = layers * sum(4 * (n + k) for n, k in layer_shapes) + 4 * (V + H)
     # correctness: the lm_head and the last layer's down projection, every output
-    import oracle  # the checker
+    import oracle  # the oracle: the reference results
     chk = {}
     fakhip.call("fhip_q4k_matmul_f32", head.ptrs[0], xs[H].ptr, ys[V].ptr, V, H, 1)
     chk["lm_head"] = check(ys[V].host(), oracle.q4k_matrows(head.raw, V, H, xs_host[H],
@@ -706,7 +706,7 @@ def cpu_baselines(c2_in, c1_in=None, c3_in=None, c4_in=None, c5_in=None):
     """The oracle (the C restatement of the reference's Go CPU path: q4kMatRowsRange /
     q4kGemmRange / kQuantMatRowsRange, row-parallel like parForRange) on the same inputs as each
     GPU workload, on cpu_threads() host threads."""
-    import oracle  # the checker, here the timed CPU path
+    import oracle  # the oracle, here the timed CPU path
     W = cpu_threads()
     q4k_rows = lambda raw, n, k, x: oracle.q4k_matrows(raw, n, k, x, workers=W)
     # C2: the decode pair
@@ -771,7 +771,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+        print(f"bench.py measures one GPU: this library has no multi-GPU path (asked for "
               f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
