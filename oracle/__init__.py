@@ -1,8 +1,8 @@
 """The oracle: ctypes access to the C restatement of fak's Go Q4_K / Q8_0 CPU path.
 
 TEST INFRASTRUCTURE ONLY. Only tests/, ``__graft_entry__.smoke()`` and bench.py's
-``cpu_baseline`` leg may import this package, and only as the checker (or the timed CPU
-baseline). The product (``fak_amd``) never loads it.
+``cpu_baseline`` leg may import this package, and only to check results against (or as the
+timed CPU baseline). The product (``fak_amd``) never loads it.
 
 Each wrapper names the reference function it restates; the C file carries the file:line
 citations.

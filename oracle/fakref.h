@@ -1,5 +1,5 @@
 /* fakref.h — the ORACLE: a plain-C restatement of fak's Go CPU path for the GGUF Q4_K / Q8_0
- * dequantize-and-multiply. TEST INFRASTRUCTURE ONLY: it is the parity checker for the HIP
+ * dequantize-and-multiply. TEST INFRASTRUCTURE ONLY: it is the parity reference for the HIP
  * backend and the CPU baseline timed beside it. Nothing in the product (fak_amd/, include/)
  * links, loads or calls it.
  *
