@@ -49,7 +49,7 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16 MFMA
 ROTATE_BYTES = 300 << 20    # > 256 MB Infinity Cache
 MIN_COPIES = 9              # at least this many distinct weight copies per rotating workload
-CPU_THREADS_MAX = 16        # worker-pool cap: the host-CPU share of one GPU on the benchmark boxes
+CPU_THREADS_MAX = 16        # worker-pool cap: one GPU's 16-core share of an 8-GPU MI355X host
 METRIC = "Q4_K decode GEMV HBM GB/s (% peak); prefill GEMM TFLOP/s (% MFMA peak)"
 
 
@@ -673,8 +673,8 @@ def nproc():
 
 def cpu_threads():
     """Threads of the CPU legs: nproc, the reference's worker count (parallel.go:31-34), capped at
-    the 16-core host share one GPU has on the benchmark boxes (the cap binds only where more
-    cores are visible than that share)."""
+    one GPU's 16-core share of an 8-GPU MI355X host (the cap binds only where more cores are
+    visible than that share)."""
     return max(1, min(nproc(), CPU_THREADS_MAX))
 
 

@@ -854,7 +854,7 @@ GemmPlan plan_gemm32(int fmt, int N, int K, int M) {
   const int cus = cu_count() > 0 ? cu_count() : 256;
   // The staged kernel from eight token tiles (M > 896) takes 256-row workgroups (four waves of
   // 64 rows, two workgroups per CU): each staged activation byte then feeds twice the MFMAs.
-  // Same box, Q4_K gate/up shape, M = 1024 / 2048 / 4096: 175-178 / 320 / 582 us against
+  // One MI355X, Q4_K gate/up shape, M = 1024 / 2048 / 4096: 175-178 / 320 / 582 us against
   // 181-183 / 333-337 / 618-621 with 128-row tiles; the down shape at M=2048 361 against 371;
   // Q6_K gate/up at M = 1024 / 2048 207-210 / 374 against 215 / 381, down 231 / 413 against
   // 242 / 440. With fewer token tiles the uneven spread of fewer, larger tiles costs more
